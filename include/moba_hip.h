@@ -1,0 +1,108 @@
+/*
+ * moba_hip.h -- C ABI of libmoba_hip.so, the gfx950 MoBA sparse block
+ * attention kernels.
+ *
+ * Conventions shared by every entry point:
+ *   - All pointers are DEVICE pointers unless stated otherwise; the library
+ *     never allocates, frees or synchronises.  Workspaces are passed in.
+ *   - `stream` is a hipStream_t (void* here to keep the header HIP-free); all
+ *     work is enqueued on it, so every call is capturable into a hipGraph.
+ *   - `dtype`: 0 = bf16, 1 = fp16 (16-bit element storage).
+ *   - Tensors are dense row-major with the shapes given; [T,H,D] means
+ *     element (t,h,d) at ((t*H)+h)*D+d.
+ *   - Return 0 on success; otherwise a MOBA_ERR_* code and
+ *     moba_hip_last_error() describes the failure (thread-local).
+ *
+ * Each entry point names the reference interface it replaces
+ * (paths relative to the Xiaotangyuan-xty/moba-merge-cuda repository).
+ */
+#ifndef MOBA_HIP_H
+#define MOBA_HIP_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOBA_HIP_ABI_VERSION 1
+#define MOBA_OK 0
+#define MOBA_ERR_ARG 1
+#define MOBA_ERR_LAUNCH 2
+#define MOBA_ERR_CAPACITY 3
+
+/* Message of the last failed call on this thread. */
+const char* moba_hip_last_error(void);
+int moba_hip_version(void);
+
+/* ---------------------------------------------------------------- prefill */
+
+/* Chunk-mean key pooling of the F routing candidates.
+ * Replaces `keys.mean(1)` / `keys.float().mean(1)` of
+ * src/moba_opt/grouped_attention.py:48-52 (diagnostic.py:391-399).
+ * k [T,Hkv,D]; chunk_start[F] first token of each candidate chunk;
+ * precision 0 = "upstream" (mean rounded to dtype), 1 = "fp32".
+ * means [F,Hkv,D] fp32.  Canonical order: sequential fp32 sum, / chunk. */
+int moba_hip_chunk_means(const void* k, int dtype, int T, int Hkv, int D,
+                         const int* chunk_start, int F, int chunk, int precision,
+                         float* means, void* stream);
+
+/* Gate scores + mask + stable top-R of every (token, q head).
+ * Replaces the einsum/mask/topk of src/moba_opt/grouped_attention.py:55-71
+ * (diagnostic.py:401-426).  q [T,Hq,D]; means [F,Hkv,D];
+ * cu_chunk[nchunk+1], chunk_batch[nchunk], first_chunk[nchunk] (first chunk of
+ * the chunk's sequence); R = min(topk-1, F) in [1,8].
+ * sel [T,Hq,R] int32: selected global chunk ids ascending, -1 padded.
+ * gate (nullable) [F,Hq,T] fp32 masked scores (-inf where illegal). */
+int moba_hip_route_prefill(const void* q, int dtype, int T, int Hq, int Hkv, int D,
+                           const float* means, const int* cu_chunk, int nchunk,
+                           const int* chunk_batch, const int* first_chunk, int R, int F,
+                           int* sel, float* gate, void* stream);
+
+/* Expert-major row lists (expert e = f*Hkv + kvhead, rows ordered
+ * (group head, token) like grouped_attention.py:78-86).
+ * counts[E], row_off[E+1], tile_off[E+1] (tiles of block_rows rows), rows[sum
+ * counts] = (s*Hq + h)*R + j where j is the chunk's rank in sel[s,h,:].
+ * Replaces the nonzero/index_select packing of grouped_attention.py:78-94. */
+int moba_hip_pack_experts(const int* sel, int T, int Hq, int Hkv, int R,
+                          const int* cu_chunk, const int* chunk_batch, const int* cu_seqlens,
+                          const int* filtered, int F, int block_rows, int* counts,
+                          int* row_off, int* tile_off, int* rows, void* stream);
+
+/* Sparse block attention forward + global-softmax merge.
+ * Replaces OptMixedAttention.forward (src/moba_opt/mixed_attention.py:42-139):
+ * both _flash_attn_varlen_forward calls and merge_forward_cuda
+ * (src/moba_opt/ops/merge.cu:187-288).
+ * q [T,Hq,D], k/v [T,Hkv,D]; self_tiles[n_self_tiles][2] = (chunk, first row)
+ * tiles of 128 rows; sel/R, filtered[F] and the pack_experts outputs describe
+ * the remote rows (R = 0: self branch only, e.g. the full-causal fallback with
+ * one chunk per sequence).  max_remote_tiles bounds tile_off[E].
+ * part_o [T*Hq*R, D] fp32 and part_lse [T*Hq*R] are workspaces.
+ * out [T,Hq,D] (dtype), lse [T,Hq] fp32 natural-log global LSE. */
+int moba_hip_prefill_fwd(const void* q, const void* k, const void* v, int dtype, int T, int Hq,
+                         int Hkv, int D, float scale, const int* cu_chunk, const int* self_tiles,
+                         int n_self_tiles, const int* sel, int R, const int* filtered, int E,
+                         const int* tile_off, const int* row_off, const int* counts,
+                         const int* rows, int max_remote_tiles, float* part_o, float* part_lse,
+                         void* out, float* lse, void* stream);
+
+/* Backward of moba_hip_prefill_fwd with the GLOBAL O and LSE.
+ * Replaces OptMixedAttention.backward (src/moba_opt/mixed_attention.py:141-225):
+ * both _flash_attn_varlen_backward calls plus the autograd scatter of the
+ * packed remote grads (grouped_attention.py:81-89).  out/dout [T,Hq,D],
+ * lse [T,Hq] from the forward; kv_tiles[n_kv_tiles][3] = (chunk, first key,
+ * filtered index or -1) tiles of 128 keys (64 when D > 128).  delta [T*Hq] and
+ * part_dq [T*Hq*R, D] fp32 are workspaces.  dq [T,Hq,D], dk/dv [T,Hkv,D]
+ * (dtype) are fully written (every key belongs to exactly one kv tile).
+ * Deterministic: no atomics, fixed reduction order. */
+int moba_hip_prefill_bwd(const void* q, const void* k, const void* v, const void* out,
+                         const void* dout, const float* lse, int dtype, int T, int Hq, int Hkv,
+                         int D, float scale, const int* cu_chunk, const int* self_tiles,
+                         int n_self_tiles, const int* kv_tiles, int n_kv_tiles, const int* sel,
+                         int R, const int* filtered, int E, const int* tile_off,
+                         const int* row_off, const int* counts, const int* rows,
+                         int max_remote_tiles, float* delta, float* part_dq, void* dq, void* dk,
+                         void* dv, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MOBA_HIP_H */

@@ -1,0 +1,64 @@
+"""Build libmoba_hip.so (gfx950) in-tree with hipcc.
+
+Every ``csrc/*.hip`` file is compiled to an object under ``_build/`` and
+linked into ``moba_hip/libmoba_hip.so``.  Objects are rebuilt when their
+source or any header changed.  ``python build.py`` builds; ``--force``
+rebuilds everything.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+CSRC = ROOT / "csrc"
+OUT_DIR = ROOT / "_build"
+LIB = ROOT / "moba_hip" / "libmoba_hip.so"
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+
+FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    "-ffp-contract=off",
+    # packed fp32 ops are disabled on this pool (device-side flag; the host
+    # pass warns that it does not know the feature).
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-result",
+]
+
+
+def _headers():
+    hs = list(CSRC.glob("*.h")) + list((ROOT.parent / "include").glob("*.h"))
+    return max((h.stat().st_mtime for h in hs), default=0.0)
+
+
+def _compile(src: Path, force: bool) -> Path:
+    obj = OUT_DIR / (src.stem + ".o")
+    if force or not obj.exists() or obj.stat().st_mtime < max(src.stat().st_mtime, _headers()):
+        cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode:
+            sys.stderr.write(r.stdout + r.stderr)
+            raise RuntimeError(f"hipcc failed on {src.name}")
+    return obj
+
+
+def build(force: bool = False, jobs: int = 8) -> Path:
+    OUT_DIR.mkdir(exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(lambda s: _compile(s, force), sources))
+    newest = max(o.stat().st_mtime for o in objs)
+    if force or not LIB.exists() or LIB.stat().st_mtime < newest:
+        tmp = LIB.with_suffix(f".so.{os.getpid()}")
+        cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+        subprocess.check_call(cmd)
+        os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(force="--force" in sys.argv))

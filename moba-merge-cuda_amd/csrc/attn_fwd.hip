@@ -1,0 +1,311 @@
+// MoBA prefill forward on gfx950: bf16/fp16 MFMA attention tiles.
+//
+// Replaces the two flash-attention forwards and the merge of
+// src/moba_opt/mixed_attention.py:67-112 (self branch: causal within each
+// chunk; remote branch: each selected (query, head) row attends one full past
+// chunk) and the atomic slot build + warp-per-row merge of
+// src/moba_opt/ops/merge.cu:27-153.
+//
+// Two launches, no atomics, no packed copies of Q or K/V:
+//  * remote_kernel: one workgroup per tile of <=128 rows of one expert
+//    (filtered chunk, kv head).  Rows are read in place from q[T,Hq,D] through
+//    the expert's row list; the chunk's K/V tiles are staged in LDS once per
+//    workgroup.  Each row writes a normalised partial (o, lse) into its slot
+//    (s*Hq + h)*R + j, j = rank of the chunk in the row's ascending selection.
+//  * self_kernel: one workgroup per (chunk, q head, 128 consecutive rows),
+//    causal within the chunk; its epilogue merges the row's partials in
+//    ascending-slot order (global softmax: m = max l, O = sum e^{l-m} o / z,
+//    L = m + log z) and writes the final O (input dtype) and LSE (fp32).
+//
+// Tile math (per wave: 32 query rows, key tiles of 64):
+//   S^T = K Q^T      (A = K rows from LDS, B = Q fragment in registers)
+//   O^T += V^T P^T   (A = V^T from a transposed LDS tile, B = P from the S^T
+//                     accumulators: the D-layout of S^T already is the B-layout
+//                     of P^T up to a fixed key permutation, applied when V^T is
+//                     written to LDS)
+// so every per-query quantity (running max, sum, rescale) is lane-uniform.
+#include "common.h"
+#include "../../include/moba_hip.h"
+
+using namespace moba;
+
+namespace {
+
+struct FwdArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  int T, Hq, Hkv, D, G;
+  float scale_log2;
+  const int* cu_chunk;
+  const int* self_tiles;
+  const int* sel;
+  int R;
+  const int* filtered;
+  int E;
+  const int* tile_off;
+  const int* row_off;
+  const int* counts;
+  const int* rows;
+  float* part_o;
+  float* part_lse;
+  uint16_t* out;
+  float* lse;
+};
+
+constexpr int kBM = 128;
+constexpr int kBN = 64;
+
+template <int DT, int DP, bool REMOTE>
+__global__ __launch_bounds__(256, 1) void fwd_kernel(FwdArgs a) {
+  constexpr int KS = DP + 8;   // K row stride (elements) in LDS
+  constexpr int VS = kBN + 8;  // V^T row stride
+  constexpr int NKS = DP / 16; // k-steps of the QK^T contraction
+  constexpr int NDB = DP / 32; // 32-row d blocks of O^T
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[kBN * KS];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[DP * VS];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int qi = lane & 31, hh = lane >> 5;
+  const int D = a.D;
+
+  int s, h, kh, k_lo, k_hi, slot = 0;
+  bool valid;
+  if constexpr (REMOTE) {
+    const int t = blockIdx.x;
+    if (t >= a.tile_off[a.E]) return;
+    int lo = 0, hi = a.E - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (a.tile_off[mid] <= t) lo = mid; else hi = mid - 1;
+    }
+    const int e = lo;
+    kh = e % a.Hkv;
+    const int c = a.filtered[e / a.Hkv];
+    k_lo = a.cu_chunk[c];
+    k_hi = a.cu_chunk[c + 1];
+    const int local = (t - a.tile_off[e]) * kBM + wave * 32 + qi;
+    valid = local < a.counts[e];
+    slot = valid ? a.rows[a.row_off[e] + local] : 0;
+    const int sh = slot / a.R;
+    s = sh / a.Hq;
+    h = sh % a.Hq;
+  } else {
+    const int c = a.self_tiles[2 * blockIdx.x], row0 = a.self_tiles[2 * blockIdx.x + 1];
+    h = blockIdx.y;
+    kh = h / a.G;
+    k_lo = a.cu_chunk[c];
+    const int c_end = a.cu_chunk[c + 1];
+    k_hi = min(c_end, k_lo + row0 + kBM);
+    s = k_lo + row0 + wave * 32 + qi;
+    valid = s < c_end;
+    if (!valid) s = k_hi - 1;
+  }
+
+  const int64_t qrow = ((int64_t)s * a.Hq + h) * D;
+  u16x8_t qf[NKS];
+#pragma unroll
+  for (int ks = 0; ks < NKS; ++ks) {
+    const int d = ks * 16 + hh * 8;
+    qf[ks] = (valid && d < D) ? ld8(a.q + qrow + d) : zero8();
+  }
+
+  f32x16_t oacc[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) oacc[db] = zero16();
+  float m_run = -INFINITY, lsum = 0.0f;
+
+  for (int kt0 = k_lo; kt0 < k_hi; kt0 += kBN) {
+    __syncthreads();
+    for (int id = tid; id < kBN * (DP / 8); id += 256) {
+      const int key = id / (DP / 8), dc = (id % (DP / 8)) * 8;
+      const int kg = kt0 + key;
+      const bool ok = kg < k_hi && dc < D;
+      const int64_t off = ((int64_t)kg * a.Hkv + kh) * D + dc;
+      const u16x8_t kv = ok ? ld8(a.k + off) : zero8();
+      const u16x8_t vv = ok ? ld8(a.v + off) : zero8();
+      st8(&Ks[key * KS + dc], kv);
+      const int pos = (key & ~15) + kperm16(key & 15);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) Vt[(dc + e) * VS + pos] = vv[e];
+    }
+    __syncthreads();
+
+    f32x16_t sacc[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      sacc[kb] = zero16();
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        const u16x8_t av = ld8(&Ks[(kb * 32 + qi) * KS + ks * 16 + hh * 8]);
+        sacc[kb] = mfma32<DT>(av, qf[ks], sacc[kb]);
+      }
+    }
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kt0 + kb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
+        const bool ok = key < k_hi && (REMOTE || key <= s);
+        const float x = ok ? sacc[kb][r] * a.scale_log2 : -INFINITY;
+        sacc[kb][r] = x;
+        mloc = fmaxf(mloc, x);
+      }
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+    const float m_new = fmaxf(m_run, mloc);
+    const float alpha = exp2f(m_run - m_new);
+    float ps = 0.0f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = exp2f(sacc[kb][r] - m_new);
+        sacc[kb][r] = p;
+        ps += p;
+      }
+    lsum = lsum * alpha + ps;
+    m_run = m_new;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+
+    u16x8_t pv[2][2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        float tmp[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) tmp[e] = sacc[kb][8 * t + e];
+        pv[kb][t] = pack8<DT>(tmp);
+      }
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const u16x8_t av = ld8(&Vt[(db * 32 + qi) * VS + kb * 32 + t * 16 + hh * 8]);
+          oacc[db] = mfma32<DT>(av, pv[kb][t], oacc[db]);
+        }
+  }
+
+  const float l = lsum + __shfl_xor(lsum, 32, 64);
+  const float L2 = m_run + log2f(l);
+  if (!valid) return;
+
+  if constexpr (REMOTE) {
+    const float inv = 1.0f / l;
+    float* po = a.part_o + (int64_t)slot * D;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d0 = db * 32 + 8 * j + 4 * hh;
+        if (d0 < D) {
+          f32x4_t o;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[i] = oacc[db][4 * j + i] * inv;
+          *reinterpret_cast<f32x4_t*>(po + d0) = o;
+        }
+      }
+    if (hh == 0) a.part_lse[slot] = L2 * kLn2;
+  } else {
+    const int64_t row = (int64_t)s * a.Hq + h;
+    float M2 = L2;
+    for (int jj = 0; jj < a.R; ++jj)
+      if (a.sel[row * a.R + jj] >= 0) M2 = fmaxf(M2, a.part_lse[row * a.R + jj] * kLog2e);
+    const float ws = exp2f(L2 - M2);
+    float z = ws;
+    const float cs = ws / l;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) oacc[db][r] *= cs;
+    for (int jj = 0; jj < a.R; ++jj) {
+      if (a.sel[row * a.R + jj] < 0) continue;
+      const int64_t sl = row * a.R + jj;
+      const float w = exp2f(a.part_lse[sl] * kLog2e - M2);
+      z += w;
+      const float* po = a.part_o + sl * D;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int d0 = db * 32 + 8 * j + 4 * hh;
+          if (d0 < D) {
+            const f32x4_t o = *reinterpret_cast<const f32x4_t*>(po + d0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) oacc[db][4 * j + i] += w * o[i];
+          }
+        }
+    }
+    const float invz = 1.0f / z;
+    uint16_t* orow = a.out + row * D;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d0 = db * 32 + 8 * j + 4 * hh;
+        if (d0 < D) {
+          u16x4_t o;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[i] = from_f32<DT>(oacc[db][4 * j + i] * invz);
+          *reinterpret_cast<u16x4_t*>(orow + d0) = o;
+        }
+      }
+    if (hh == 0) a.lse[row] = (M2 + log2f(z)) * kLn2;
+  }
+}
+
+template <int DT, int DP>
+int launch_fwd(const FwdArgs& a, int n_self_tiles, int max_remote_tiles, hipStream_t st) {
+  if (max_remote_tiles > 0 && a.R > 0) {
+    hipLaunchKernelGGL((fwd_kernel<DT, DP, true>), dim3(max_remote_tiles), dim3(256), 0, st, a);
+    int rc = moba_launch_status("prefill_fwd(remote)");
+    if (rc) return rc;
+  }
+  if (n_self_tiles > 0) {
+    hipLaunchKernelGGL((fwd_kernel<DT, DP, false>), dim3(n_self_tiles, a.Hq), dim3(256), 0, st, a);
+    return moba_launch_status("prefill_fwd(self)");
+  }
+  return MOBA_OK;
+}
+
+template <int DT>
+int dispatch_fwd(const FwdArgs& a, int n_self, int max_remote, hipStream_t st) {
+  if (a.D <= 32) return launch_fwd<DT, 32>(a, n_self, max_remote, st);
+  if (a.D <= 64) return launch_fwd<DT, 64>(a, n_self, max_remote, st);
+  if (a.D <= 128) return launch_fwd<DT, 128>(a, n_self, max_remote, st);
+  return launch_fwd<DT, 256>(a, n_self, max_remote, st);
+}
+
+}  // namespace
+
+extern "C" int moba_hip_prefill_fwd(const void* q, const void* k, const void* v, int dtype, int T,
+                                    int Hq, int Hkv, int D, float scale, const int* cu_chunk,
+                                    const int* self_tiles, int n_self_tiles, const int* sel, int R,
+                                    const int* filtered, int E, const int* tile_off,
+                                    const int* row_off, const int* counts, const int* rows,
+                                    int max_remote_tiles, float* part_o, float* part_lse,
+                                    void* out, float* lse, void* stream) {
+  if (dtype != 0 && dtype != 1) { moba_set_error("prefill_fwd: dtype must be 0 (bf16) or 1 (fp16)"); return MOBA_ERR_ARG; }
+  if (D < 8 || D > 256 || D % 8) { moba_set_error("prefill_fwd: head_dim must be a multiple of 8 in [8,256]"); return MOBA_ERR_ARG; }
+  if (Hq < 1 || Hkv < 1 || Hq % Hkv) { moba_set_error("prefill_fwd: Hq must be a positive multiple of Hkv"); return MOBA_ERR_ARG; }
+  if (R < 0 || R > 8) { moba_set_error("prefill_fwd: remote count must be in [0,8]"); return MOBA_ERR_ARG; }
+  if (Hq > 65535) { moba_set_error("prefill_fwd: too many heads"); return MOBA_ERR_ARG; }
+  FwdArgs a;
+  a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v;
+  a.T = T; a.Hq = Hq; a.Hkv = Hkv; a.D = D; a.G = Hq / Hkv;
+  a.scale_log2 = scale * kLog2e;
+  a.cu_chunk = cu_chunk; a.self_tiles = self_tiles;
+  a.sel = sel; a.R = R; a.filtered = filtered; a.E = E;
+  a.tile_off = tile_off; a.row_off = row_off; a.counts = counts; a.rows = rows;
+  a.part_o = part_o; a.part_lse = part_lse;
+  a.out = (uint16_t*)out; a.lse = lse;
+  hipStream_t st = (hipStream_t)stream;
+  return dtype == 0 ? dispatch_fwd<0>(a, n_self_tiles, R > 0 ? max_remote_tiles : 0, st)
+                    : dispatch_fwd<1>(a, n_self_tiles, R > 0 ? max_remote_tiles : 0, st);
+}

@@ -1,0 +1,109 @@
+// Shared device helpers for the gfx950 MoBA kernels.
+//
+// Element storage is raw 16-bit (bf16 = dtype 0, fp16 = dtype 1).  MFMA tiles
+// use v_mfma_f32_32x32x16_{bf16,f16}; the operand layouts (verified on gfx950):
+//   A[m][k] : lane l supplies row m = l%32, k = (l/32)*8 + e, e = 0..7
+//   B[k][n] : lane l supplies col n = l%32, k = (l/32)*8 + e
+//   D[m][n] : lane l holds   col n = l%32, rows m = 8*j + 4*(l/32) + i  (value j*4+i)
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define MOBA_DEV __device__ __forceinline__
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint16_t u16x8_t __attribute__((ext_vector_type(8)));
+typedef uint16_t u16x4_t __attribute__((ext_vector_type(4)));
+
+namespace moba {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+MOBA_DEV float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// Round-to-nearest-even float -> bf16 (same bit recipe as the CPU oracle).
+MOBA_DEV uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+MOBA_DEV float f16_to_f32(uint16_t h) {
+  _Float16 x = __builtin_bit_cast(_Float16, h);
+  return (float)x;
+}
+MOBA_DEV uint16_t f32_to_f16(float f) {
+  _Float16 x = (_Float16)f;  // v_cvt_f16_f32, round-to-nearest-even
+  return __builtin_bit_cast(uint16_t, x);
+}
+
+template <int DT> MOBA_DEV float to_f32(uint16_t v) {
+  if constexpr (DT == 0) return bf16_to_f32(v); else return f16_to_f32(v);
+}
+template <int DT> MOBA_DEV uint16_t from_f32(float v) {
+  if constexpr (DT == 0) return f32_to_bf16(v); else return f32_to_f16(v);
+}
+
+// 32x32x16 MFMA on 8 packed 16-bit elements per lane.
+template <int DT>
+MOBA_DEV f32x16_t mfma32(const u16x8_t& a, const u16x8_t& b, const f32x16_t& c) {
+  if constexpr (DT == 0) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+}
+
+MOBA_DEV f32x16_t zero16() {
+  f32x16_t z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.0f;
+  return z;
+}
+
+MOBA_DEV u16x8_t zero8() {
+  u16x8_t z;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) z[i] = 0;
+  return z;
+}
+
+MOBA_DEV u16x8_t ld8(const uint16_t* p) { return *reinterpret_cast<const u16x8_t*>(p); }
+MOBA_DEV void st8(uint16_t* p, const u16x8_t& v) { *reinterpret_cast<u16x8_t*>(p) = v; }
+
+// Position of key r (0..15) of a 16-key MFMA k-group inside a transposed LDS
+// row.  A 32-key score block held as D-layout gives lane half h the keys
+// {4h..4h+3, 8+4h..8+4h+3} of each 16-key group; storing key r at this
+// position makes those 8 keys contiguous at offset 8h.
+MOBA_DEV int kperm16(int r) { return ((r >> 2) & 1) * 8 + ((r >> 3) & 1) * 4 + (r & 3); }
+
+template <int DT> MOBA_DEV u16x8_t pack8(const float* v) {
+  u16x8_t r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = from_f32<DT>(v[e]);
+  return r;
+}
+
+MOBA_DEV float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+MOBA_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+}  // namespace moba
+
+// Error reporting shared by the C-ABI entry points.
+void moba_set_error(const char* fmt, ...);
+int moba_launch_status(const char* what);

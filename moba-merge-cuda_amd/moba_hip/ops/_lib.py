@@ -1,0 +1,77 @@
+"""ctypes binding of libmoba_hip.so (the C ABI declared in include/moba_hip.h).
+
+The shared library is loaded from the package directory.  There is no fallback:
+if the library is missing every op raises, so a GPU run can never silently use
+another implementation.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parents[1] / "libmoba_hip.so"
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+
+# name -> argtypes (restype int unless listed in _RESTYPES)
+SIGNATURES = {
+    "moba_hip_version": [],
+    "moba_hip_last_error": [],
+    "moba_hip_chunk_means": [_P, _I, _I, _I, _I, _P, _I, _I, _I, _P, _P],
+    "moba_hip_route_prefill": [_P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _I, _I, _P, _P, _P],
+    "moba_hip_pack_experts": [_P, _I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _P, _P, _P, _P, _P],
+    "moba_hip_prefill_fwd": [_P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _I, _P, _I, _P, _I,
+                             _P, _P, _P, _P, _I, _P, _P, _P, _P, _P],
+    "moba_hip_prefill_bwd": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _I, _P, _I,
+                             _P, _I, _P, _I, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P],
+}
+_RESTYPES = {"moba_hip_last_error": ctypes.c_char_p}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class MobaHipError(RuntimeError):
+    pass
+
+
+def load():
+    """Load the library (once).  Raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise MobaHipError(
+                    f"{LIB_PATH} is missing: build it with `python moba-merge-cuda_amd/build.py` "
+                    "(or __graft_entry__.build()); there is no fallback implementation")
+            lib = ctypes.CDLL(str(LIB_PATH))
+            for name, args in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.argtypes = args
+                fn.restype = _RESTYPES.get(name, ctypes.c_int)
+            _lib = lib
+    return _lib
+
+
+def call(name: str, *args) -> None:
+    """Invoke an entry point and raise MobaHipError on a non-zero status."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.moba_hip_last_error().decode(errors="replace")
+        raise MobaHipError(f"{name} failed ({rc}): {msg}")
+
+
+def ptr(t) -> int | None:
+    """Device address of a torch tensor (None for None)."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(device) -> int:
+    import torch
+    return torch.cuda.current_stream(device).cuda_stream

@@ -1,0 +1,186 @@
+"""Host side of the prefill path: chunk metadata and the kernel launch sequence.
+
+``PrefillPlan`` restates calc_chunks (src/moba_opt/diagnostic.py:30-80) on the
+host copy of cu_seqlens that validation already read, adds the tile lists the
+kernels need, and uploads everything in one int32 buffer.  Plans are cached by
+(cu_seqlens values, chunk, heads, device) -- the reference caches calc_chunks
+by tensor object (lru_cache, diagnostic.py:30).
+"""
+from __future__ import annotations
+
+from collections import OrderedDict
+
+import torch
+
+from . import _lib
+
+BLOCK_ROWS = 128  # query rows per attention workgroup (4 waves x 32)
+DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1}
+
+
+class PrefillPlan:
+    """Chunk metadata + tile lists for one (cu_seqlens, chunk, Hq, Hkv) shape."""
+
+    def __init__(self, cu, chunk, hq, hkv, head_dim, topk, device, fallback=False):
+        self.cu = list(cu)
+        self.head_dim = head_dim
+        self.chunk = chunk
+        self.hq, self.hkv = hq, hkv
+        self.groups = hq // hkv
+        cu_chunk, chunk_batch, filtered = [0], [], []
+        for b in range(len(cu) - 1):
+            length = cu[b + 1] - cu[b]
+            n = (length + chunk - 1) // chunk
+            for i in range(n):
+                if i + 1 < n:
+                    filtered.append(len(chunk_batch))
+                chunk_batch.append(b)
+                cu_chunk.append(cu_chunk[-1] + min(chunk, length - i * chunk))
+        self.cu_chunk, self.chunk_batch, self.filtered = cu_chunk, chunk_batch, filtered
+        self.num_filtered = len(filtered)
+        self.remote = min(topk - 1, self.num_filtered)
+        self.fallback = fallback or self.remote == 0
+        if self.fallback:
+            # k=1 / no-candidate fallback: full causal attention per sequence
+            # (grouped_attention.py:41-46) == one "chunk" per sequence, no remote.
+            att_chunk = list(cu)
+            self.remote = 0
+        else:
+            att_chunk = cu_chunk
+        first = []
+        for c, b in enumerate(chunk_batch):
+            first.append(c if c == 0 or chunk_batch[c - 1] != b else first[-1])
+        tiles = []
+        for c in range(len(att_chunk) - 1):
+            length = att_chunk[c + 1] - att_chunk[c]
+            tiles.extend((c, r0) for r0 in range(0, length, BLOCK_ROWS))
+        tiles.sort(key=lambda x: -x[1])  # most keys first
+        self.n_self_tiles = len(tiles)
+        self.num_experts = self.num_filtered * hkv
+        max_tiles = 0
+        for c in filtered:
+            ns = cu[chunk_batch[c] + 1] - cu_chunk[c + 1]
+            max_tiles += hkv * ((self.groups * ns + BLOCK_ROWS - 1) // BLOCK_ROWS)
+        self.max_remote_tiles = max_tiles
+        self.chunk_start = [cu_chunk[c] for c in filtered]
+        # key-major backward tiles: (chunk, first key, filtered index or -1)
+        self.kv_block = 64 if self.head_dim > 128 else 128
+        fidx = {c: i for i, c in enumerate(filtered)}
+        kv = []
+        for c in range(len(att_chunk) - 1):
+            length = att_chunk[c + 1] - att_chunk[c]
+            f = -1 if self.fallback else fidx.get(c, -1)
+            tail = 0 if f < 0 else cu[chunk_batch[c] + 1] - cu_chunk[c + 1]
+            kv.extend((tail, k0, c, f) for k0 in range(0, length, self.kv_block))
+        kv.sort(key=lambda x: (-x[0], x[1]))  # most expert rows first, then most causal rows
+        self.n_kv_tiles = len(kv)
+        kv_flat = [x for t in kv for x in t[2:3] + t[1:2] + t[3:4]]
+
+        parts = OrderedDict(
+            att_chunk=att_chunk, cu_chunk=cu_chunk, chunk_batch=chunk_batch, first_chunk=first,
+            cu_seqlens=list(cu), filtered=filtered or [0], chunk_start=self.chunk_start or [0],
+            self_tiles=[x for t in tiles for x in t] or [0, 0], kv_tiles=kv_flat or [0, 0, -1])
+        flat, self._views = [], {}
+        for name, vals in parts.items():
+            self._views[name] = (len(flat), len(vals))
+            flat.extend(vals)
+        self.meta = torch.tensor(flat, dtype=torch.int32).to(device, non_blocking=False)
+
+    def dev(self, name):
+        off, n = self._views[name]
+        return self.meta[off:off + n]
+
+    def ptr(self, name):
+        return self.dev(name).data_ptr()
+
+
+_PLANS: "OrderedDict[tuple, PrefillPlan]" = OrderedDict()
+
+
+def get_plan(cu, chunk, hq, hkv, head_dim, topk, device, fallback=False):
+    key = (tuple(cu), chunk, hq, hkv, head_dim, topk, str(device), fallback)
+    plan = _PLANS.get(key)
+    if plan is None:
+        plan = PrefillPlan(cu, chunk, hq, hkv, head_dim, topk, device, fallback)
+        _PLANS[key] = plan
+        if len(_PLANS) > 16:
+            _PLANS.popitem(last=False)
+    else:
+        _PLANS.move_to_end(key)
+    return plan
+
+
+class RouteResult:
+    """Device routing state shared by the forward and the backward."""
+    __slots__ = ("sel", "counts", "row_off", "tile_off", "rows", "means")
+
+
+def route(plan: PrefillPlan, q, k, precision: int, want_gate=False):
+    """Chunk means, gate + stable top-k, expert packing.  Returns RouteResult
+    (and the masked gate [F,Hq,T] when ``want_gate``)."""
+    T, hq, d = q.shape
+    dev = q.device
+    st = _lib.stream_of(dev)
+    code = DTYPE_CODE[q.dtype]
+    r = RouteResult()
+    F, R, E = plan.num_filtered, plan.remote, plan.num_experts
+    r.means = torch.empty((F, plan.hkv, d), dtype=torch.float32, device=dev)
+    r.sel = torch.empty((T, hq, R), dtype=torch.int32, device=dev)
+    r.counts = torch.empty(E, dtype=torch.int32, device=dev)
+    r.row_off = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    r.tile_off = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    r.rows = torch.empty(max(1, T * hq * R), dtype=torch.int32, device=dev)
+    gate = torch.empty((F, hq, T), dtype=torch.float32, device=dev) if want_gate else None
+    _lib.call("moba_hip_chunk_means", k.data_ptr(), code, T, plan.hkv, d,
+              plan.ptr("chunk_start"), F, plan.chunk, precision, r.means.data_ptr(), st)
+    _lib.call("moba_hip_route_prefill", q.data_ptr(), code, T, hq, plan.hkv, d,
+              r.means.data_ptr(), plan.ptr("cu_chunk"), len(plan.chunk_batch),
+              plan.ptr("chunk_batch"), plan.ptr("first_chunk"), R, F, r.sel.data_ptr(),
+              _lib.ptr(gate), st)
+    _lib.call("moba_hip_pack_experts", r.sel.data_ptr(), T, hq, plan.hkv, R,
+              plan.ptr("cu_chunk"), plan.ptr("chunk_batch"), plan.ptr("cu_seqlens"),
+              plan.ptr("filtered"), F, BLOCK_ROWS, r.counts.data_ptr(), r.row_off.data_ptr(),
+              r.tile_off.data_ptr(), r.rows.data_ptr(), st)
+    return (r, gate) if want_gate else r
+
+
+def forward(plan: PrefillPlan, q, k, v, rt: RouteResult | None):
+    """Sparse attention + merge.  Returns (out [T,Hq,D], lse [T,Hq] fp32)."""
+    T, hq, d = q.shape
+    dev = q.device
+    R = plan.remote
+    out = torch.empty_like(q)
+    lse = torch.empty((T, hq), dtype=torch.float32, device=dev)
+    part_o = part_lse = None
+    if R:
+        part_o = torch.empty((T * hq * R, d), dtype=torch.float32, device=dev)
+        part_lse = torch.empty(T * hq * R, dtype=torch.float32, device=dev)
+    _lib.call("moba_hip_prefill_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(),
+              DTYPE_CODE[q.dtype], T, hq, plan.hkv, d, d ** -0.5,
+              plan.ptr("att_chunk"), plan.ptr("self_tiles"), plan.n_self_tiles,
+              _lib.ptr(rt.sel) if R else None, R, plan.ptr("filtered"), plan.num_experts,
+              _lib.ptr(rt.tile_off) if R else None, _lib.ptr(rt.row_off) if R else None,
+              _lib.ptr(rt.counts) if R else None, _lib.ptr(rt.rows) if R else None,
+              plan.max_remote_tiles if R else 0, _lib.ptr(part_o), _lib.ptr(part_lse),
+              out.data_ptr(), lse.data_ptr(), _lib.stream_of(dev))
+    return out, lse
+
+
+def backward(plan: PrefillPlan, q, k, v, out, lse, dout, rt: RouteResult | None):
+    """Gradients (dq, dk, dv) of ``forward`` for the upstream gradient ``dout``."""
+    T, hq, d = q.shape
+    dev = q.device
+    R = plan.remote
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    delta = torch.empty(T * hq, dtype=torch.float32, device=dev)
+    part_dq = torch.empty((T * hq * R, d), dtype=torch.float32, device=dev) if R else None
+    _lib.call("moba_hip_prefill_bwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+              dout.data_ptr(), lse.data_ptr(), DTYPE_CODE[q.dtype], T, hq, plan.hkv, d,
+              d ** -0.5, plan.ptr("att_chunk"), plan.ptr("self_tiles"), plan.n_self_tiles,
+              plan.ptr("kv_tiles"), plan.n_kv_tiles,
+              _lib.ptr(rt.sel) if R else None, R, plan.ptr("filtered"), plan.num_experts,
+              _lib.ptr(rt.tile_off) if R else None, _lib.ptr(rt.row_off) if R else None,
+              _lib.ptr(rt.counts) if R else None, _lib.ptr(rt.rows) if R else None,
+              plan.max_remote_tiles if R else 0, delta.data_ptr(), _lib.ptr(part_dq),
+              dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), _lib.stream_of(dev))
+    return dq, dk, dv

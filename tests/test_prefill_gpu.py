@@ -1,0 +1,113 @@
+"""GPU parity of the prefill path against the CPU oracle.
+
+Routing (means, gate scores, selected blocks) must be bit-identical to the
+canonical oracle; outputs and gradients must be within the north-star
+tolerance of the FP64 fixed-route oracle evaluated on the SAME routes
+(bf16: max-abs <= 2e-2, mean-abs <= 2e-3; fp16: 4e-3 / 4e-4).
+Shapes follow the reference's GQA matrix (tests/test_grouped_attention.py:36-91).
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import TOL, assert_close_stats, oracle_route, prefill_inputs
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(q, k, v, cu, ml, cfg):
+    import moba_hip  # noqa: F401
+    from moba_hip.ops import prefill as P
+    from moba_hip.grouped_attention import moba_hip_attention
+    qr, kr, vr = (x.detach().requires_grad_(True) for x in (q, k, v))
+    out, lse = moba_hip_attention(qr, kr, vr, cu, ml, cfg, return_lse=True)
+    plan = P.get_plan(cu.tolist(), cfg["chunk_size"], q.shape[1], k.shape[1], q.shape[2],
+                      cfg["topk"], q.device)
+    return qr, kr, vr, out, lse, plan
+
+
+def _gpu_route(q, k, cu, cfg, precision=0):
+    from moba_hip.ops import prefill as P
+    plan = P.get_plan(cu.tolist(), cfg["chunk_size"], q.shape[1], k.shape[1], q.shape[2],
+                      cfg["topk"], q.device)
+    rt, gate = P.route(plan, q.contiguous(), k.contiguous(), precision, want_gate=True)
+    torch.cuda.synchronize()
+    return plan, rt, gate
+
+
+@pytest.mark.parametrize("precision", [0, 1])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("hq,hkv,dim,lens,chunk,topk", [
+    (4, 2, 64, (35, 62), 16, 4),
+    (8, 1, 128, (129, 257), 32, 3),
+    (14, 2, 64, (600,), 64, 3),
+    (6, 3, 40, (17, 1, 90), 8, 9),
+])
+def test_routing_bit_exact(cuda_device, hq, hkv, dim, lens, chunk, topk, dtype, precision):
+    q, k, v, cu, ml, _ = prefill_inputs(hq, hkv, dim, lens, dtype, seed=7)
+    cfg = {"chunk_size": chunk, "topk": topk}
+    plan, rt, gate = _gpu_route(q, k, cu, cfg, precision)
+    sel, means, gate_ref, (cu_chunk, _, filtered, remote) = oracle_route(q, k, cu, chunk, topk,
+                                                                        precision)
+    assert plan.remote == remote
+    np.testing.assert_array_equal(rt.means.cpu().numpy().view(np.uint32), means.view(np.uint32))
+    g = gate.cpu().numpy()
+    np.testing.assert_array_equal(np.isinf(g), np.isinf(gate_ref))
+    fin = np.isfinite(gate_ref)
+    np.testing.assert_array_equal(g[fin].view(np.uint32), gate_ref[fin].view(np.uint32))
+    np.testing.assert_array_equal(rt.sel.cpu().numpy(), sel)
+    # expert lists: every selected (s,h,j) appears exactly once, grouped by expert
+    counts = rt.counts.cpu().numpy()
+    rows = rt.rows.cpu().numpy()[: counts.sum()]
+    R = remote
+    expect = sorted(((s * hq + h) * R + j) for s in range(q.shape[0]) for h in range(hq)
+                    for j in range(R) if sel[s, h, j] >= 0)
+    assert sorted(rows.tolist()) == expect
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("hq,hkv,dim,lens,chunk,topk", [
+    (1, 1, 64, (35, 62), 16, 4),
+    (8, 2, 128, (35, 62), 16, 4),
+    (4, 2, 16, (9, 12), 4, 3),
+    (28, 4, 64, (65, 96), 16, 4),
+    (8, 1, 256, (150,), 32, 3),
+    (6, 2, 72, (200, 7), 24, 9),
+    (8, 1, 64, (35, 62), 16, 1),
+    (8, 1, 64, (1, 3), 16, 4),
+])
+def test_forward_backward_vs_fp64(cuda_device, hq, hkv, dim, lens, chunk, topk, dtype):
+    q, k, v, cu, ml, g = prefill_inputs(hq, hkv, dim, lens, dtype, seed=62)
+    cfg = {"chunk_size": chunk, "topk": topk}
+    qr, kr, vr, out, lse, plan = _run(q, k, v, cu, ml, cfg)
+    dq, dk, dv = torch.autograd.grad(out, (qr, kr, vr), grad_outputs=g)
+    if plan.fallback:
+        sel, att_chunk = None, cu.tolist()
+    else:
+        sel, _, _, (att_chunk, _, _, _) = oracle_route(q, k, cu, chunk, topk)
+    qd, kd, vd, gd = (x.detach().double().cpu().numpy() for x in (q, k, v, g))
+    o_ref, l_ref = O.attention_fwd(qd, kd, vd, att_chunk, sel)
+    assert_close_stats(out, o_ref, dtype, "out")
+    np.testing.assert_allclose(lse.cpu().numpy(), l_ref, atol=2e-3, rtol=1e-4)
+    dq_ref, dk_ref, dv_ref = O.attention_bwd(qd, kd, vd, gd, att_chunk, sel, l_ref)
+    for name, a, e in (("dq", dq, dq_ref), ("dk", dk, dk_ref), ("dv", dv, dv_ref)):
+        scale = max(1.0, float(np.abs(e).max()) / 4)
+        diff = np.abs(a.double().cpu().numpy() - e)
+        max_tol, mean_tol = TOL[dtype]
+        assert np.isfinite(diff).all(), name
+        assert diff.max() <= max_tol * scale, f"{name} max {diff.max():.3e} (scale {scale:.1f})"
+        assert diff.mean() <= mean_tol * scale, f"{name} mean {diff.mean():.3e}"
+
+
+def test_repeat_bitwise(cuda_device):
+    q, k, v, cu, ml, g = prefill_inputs(8, 2, 64, (257, 129), torch.bfloat16, seed=362)
+    cfg = {"chunk_size": 16, "topk": 4}
+    outs = []
+    for _ in range(4):
+        qr, kr, vr, out, _, _ = _run(q, k, v, cu, ml, cfg)
+        grads = torch.autograd.grad(out, (qr, kr, vr), grad_outputs=g)
+        outs.append((out.detach(),) + grads)
+    for other in outs[1:]:
+        for a, b in zip(outs[0], other):
+            assert torch.equal(a, b)
