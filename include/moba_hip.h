@@ -72,7 +72,7 @@ int moba_hip_pack_experts(const int* sel, int T, int Hq, int Hkv, int R,
  * both _flash_attn_varlen_forward calls and merge_forward_cuda
  * (src/moba_opt/ops/merge.cu:187-288).
  * q [T,Hq,D], k/v [T,Hkv,D]; self_tiles[n_self_tiles][2] = (chunk, first row)
- * tiles of 128 rows; sel/R, filtered[F] and the pack_experts outputs describe
+ * tiles of 256 rows (128 when D > 128); sel/R, filtered[F] and the pack_experts outputs describe
  * the remote rows (R = 0: self branch only, e.g. the full-causal fallback with
  * one chunk per sequence).  max_remote_tiles bounds tile_off[E].
  * part_o [T*Hq*R, D] fp32 and part_lse [T*Hq*R] are workspaces.

@@ -51,7 +51,6 @@ struct BwdArgs {
   uint16_t* dv;
 };
 
-constexpr int kBM = 128;  // dq: query rows per workgroup
 constexpr int kBN = 64;   // dq: keys per LDS tile
 constexpr int kBQ = 64;   // dkdv: query rows per LDS tile
 
@@ -65,9 +64,9 @@ __global__ __launch_bounds__(256) void delta_kernel(const uint16_t* __restrict__
   float acc = 0.0f;
   if (row < rows) {
     for (int d = sub * 8; d < D; d += 128) {
-      const u16x8_t a = ld8(o + row * D + d), b = ld8(g + row * D + d);
+      const u16x8_t x = ld8(o + row * D + d), y = ld8(g + row * D + d);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc += to_f32<DT>(a[e]) * to_f32<DT>(b[e]);
+      for (int e = 0; e < 8; ++e) acc += to_f32<DT>(x[e]) * to_f32<DT>(y[e]);
     }
   }
 #pragma unroll
@@ -76,19 +75,23 @@ __global__ __launch_bounds__(256) void delta_kernel(const uint16_t* __restrict__
 }
 
 // --------------------------------------------------------------------- dq
-template <int DT, int DP, bool REMOTE>
+// Per wave two blocks of 32 query rows; K/V tiles of 64 keys double-buffered
+// in LDS (row-major).  S^T = K Q^T and dP^T = V dO^T take K / V rows as the A
+// operand; dQ^T = K^T dS^T reads K^T with the transposed LDS read.
+template <int DT, int DP, bool REMOTE, int QB>
 __global__ __launch_bounds__(256, 1) void dq_kernel(BwdArgs a) {
-  constexpr int KS = DP + 8, TS = kBN + 8, NKS = DP / 16, NDB = DP / 32;
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[kBN * KS];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[kBN * KS];
-  __shared__ __attribute__((aligned(16))) uint16_t Kt[DP * TS];
+  constexpr int KS = DP + 8, NKS = DP / 16, NDB = DP / 32;
+  constexpr int NLD = kBN * DP / 8 / 256;
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kBN * KS];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][kBN * KS];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int qi = lane & 31, hh = lane >> 5;
   const int D = a.D;
 
-  int s, h, kh, k_lo, k_hi, slot = 0;
-  bool valid;
+  int s[QB], h[QB], slot[QB];
+  bool valid[QB];
+  int kh, k_lo, k_hi, s_wave0 = 0;
   if constexpr (REMOTE) {
     const int t = blockIdx.x;
     if (t >= a.tile_off[a.E]) return;
@@ -102,150 +105,199 @@ __global__ __launch_bounds__(256, 1) void dq_kernel(BwdArgs a) {
     const int c = a.filtered[e / a.Hkv];
     k_lo = a.cu_chunk[c];
     k_hi = a.cu_chunk[c + 1];
-    const int local = (t - a.tile_off[e]) * kBM + wave * 32 + qi;
-    valid = local < a.counts[e];
-    slot = valid ? a.rows[a.row_off[e] + local] : 0;
-    const int sh = slot / a.R;
-    s = sh / a.Hq;
-    h = sh % a.Hq;
+    const int cnt = a.counts[e], base = a.row_off[e];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const int local = (t - a.tile_off[e]) * (128 * QB) + wave * (32 * QB) + qb * 32 + qi;
+      valid[qb] = local < cnt;
+      slot[qb] = valid[qb] ? a.rows[base + local] : 0;
+      const int sh = slot[qb] / a.R;
+      s[qb] = sh / a.Hq;
+      h[qb] = sh % a.Hq;
+    }
   } else {
     const int c = a.self_tiles[2 * blockIdx.x], row0 = a.self_tiles[2 * blockIdx.x + 1];
-    h = blockIdx.y;
-    kh = h / a.G;
+    kh = blockIdx.y / a.G;
     k_lo = a.cu_chunk[c];
     const int c_end = a.cu_chunk[c + 1];
-    k_hi = min(c_end, k_lo + row0 + kBM);
-    s = k_lo + row0 + wave * 32 + qi;
-    valid = s < c_end;
-    if (!valid) s = k_hi - 1;
-  }
-  const int64_t row = (int64_t)s * a.Hq + h;
-  u16x8_t qf[NKS], gf[NKS];
+    k_hi = min(c_end, k_lo + row0 + 128 * QB);
+    s_wave0 = k_lo + row0 + wave * (32 * QB);
 #pragma unroll
-  for (int ks = 0; ks < NKS; ++ks) {
-    const int d = ks * 16 + hh * 8;
-    const bool ok = valid && d < D;
-    qf[ks] = ok ? ld8(a.q + row * D + d) : zero8();
-    gf[ks] = ok ? ld8(a.dout + row * D + d) : zero8();
+    for (int qb = 0; qb < QB; ++qb) {
+      h[qb] = blockIdx.y;
+      s[qb] = s_wave0 + qb * 32 + qi;
+      valid[qb] = s[qb] < c_end;
+      if (!valid[qb]) s[qb] = k_hi - 1;
+    }
   }
-  const float lse2 = valid ? a.lse[row] * kLog2e : INFINITY;
-  const float dl = valid ? a.delta[row] : 0.0f;
-
-  f32x16_t acc[NDB];
+  u16x8_t qf[QB][NKS], gf[QB][NKS];
+  float lse2[QB], dl[QB];
 #pragma unroll
-  for (int db = 0; db < NDB; ++db) acc[db] = zero16();
+  for (int qb = 0; qb < QB; ++qb) {
+    const int64_t row = (int64_t)s[qb] * a.Hq + h[qb];
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const int d = ks * 16 + hh * 8;
+      const bool ok = valid[qb] && d < D;
+      qf[qb][ks] = ok ? ld8(a.q + row * D + d) : zero8();
+      gf[qb][ks] = ok ? ld8(a.dout + row * D + d) : zero8();
+    }
+    lse2[qb] = valid[qb] ? a.lse[row] * kLog2e : INFINITY;
+    dl[qb] = valid[qb] ? a.delta[row] : 0.0f;
+  }
 
-  for (int kt0 = k_lo; kt0 < k_hi; kt0 += kBN) {
-    __syncthreads();
-    for (int id = tid; id < kBN * (DP / 8); id += 256) {
-      const int key = id / (DP / 8), dc = (id % (DP / 8)) * 8;
+  u16x8_t kr[NLD], vr[NLD];
+  auto gload = [&](int kt0) {
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+      const int id = tid + i * 256, key = id / (DP / 8), dc = (id % (DP / 8)) * 8;
       const int kg = kt0 + key;
       const bool ok = kg < k_hi && dc < D;
       const int64_t off = ((int64_t)kg * a.Hkv + kh) * D + dc;
-      const u16x8_t kv = ok ? ld8(a.k + off) : zero8();
-      const u16x8_t vv = ok ? ld8(a.v + off) : zero8();
-      st8(&Ks[key * KS + dc], kv);
-      st8(&Vs[key * KS + dc], vv);
-      const int pos = (key & ~15) + kperm16(key & 15);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) Kt[(dc + e) * TS + pos] = kv[e];
+      kr[i] = ok ? ld8(a.k + off) : zero8();
+      vr[i] = ok ? ld8(a.v + off) : zero8();
     }
-    __syncthreads();
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+      const int id = tid + i * 256, key = id / (DP / 8), dc = (id % (DP / 8)) * 8;
+      st8(&Ks[buf][key * KS + dc], kr[i]);
+      st8(&Vs[buf][key * KS + dc], vr[i]);
+    }
+  };
 
-    u16x8_t dsv[2][2];
+  f32x16_t acc[QB][NDB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) acc[qb][db] = zero16();
+  const float c2 = a.scale_log2;
+
+  const int ntiles = (k_hi - k_lo + kBN - 1) / kBN;
+  gload(k_lo);
+  lstore(0);
+  __syncthreads();
+  for (int it = 0; it < ntiles; ++it) {
+    const int kt0 = k_lo + it * kBN, buf = it & 1;
+    if (it + 1 < ntiles) gload(kt0 + kBN);
+    const bool need_mask = (kt0 + kBN > k_hi) || (!REMOTE && kt0 + kBN - 1 > s_wave0);
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      f32x16_t sa = zero16(), pa = zero16();
+      f32x16_t sa[QB], pa[QB];
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) { sa[qb] = zero16(); pa[qb] = zero16(); }
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {
-        sa = mfma32<DT>(ld8(&Ks[(kb * 32 + qi) * KS + ks * 16 + hh * 8]), qf[ks], sa);
-        pa = mfma32<DT>(ld8(&Vs[(kb * 32 + qi) * KS + ks * 16 + hh * 8]), gf[ks], pa);
-      }
-      float tmp[16];
+        const u16x8_t ka = ld8(&Ks[buf][(kb * 32 + qi) * KS + ks * 16 + hh * 8]);
+        const u16x8_t va = ld8(&Vs[buf][(kb * 32 + qi) * KS + ks * 16 + hh * 8]);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kt0 + kb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
-        const bool ok = key < k_hi && (REMOTE || key <= s);
-        const float p = ok ? exp2f(sa[r] * a.scale_log2 - lse2) : 0.0f;
-        tmp[r] = p * (pa[r] - dl);
-      }
-      dsv[kb][0] = pack8<DT>(tmp);
-      dsv[kb][1] = pack8<DT>(tmp + 8);
-    }
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-          acc[db] = mfma32<DT>(ld8(&Kt[(db * 32 + qi) * TS + kb * 32 + t * 16 + hh * 8]),
-                               dsv[kb][t], acc[db]);
-  }
-  if (!valid) return;
-
-  if constexpr (REMOTE) {
-    float* po = a.part_dq + (int64_t)slot * D;
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int d0 = db * 32 + 8 * j + 4 * hh;
-        if (d0 < D) {
-          f32x4_t o;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) o[i] = acc[db][4 * j + i] * a.scale;
-          *reinterpret_cast<f32x4_t*>(po + d0) = o;
+        for (int qb = 0; qb < QB; ++qb) {
+          sa[qb] = mfma32<DT>(ka, qf[qb][ks], sa[qb]);
+          pa[qb] = mfma32<DT>(va, gf[qb][ks], pa[qb]);
         }
       }
-  } else {
+      u16x8_t dsv[QB][2];
 #pragma unroll
-    for (int db = 0; db < NDB; ++db)
+      for (int qb = 0; qb < QB; ++qb) {
+        float tmp[16];
+        const float nl = -lse2[qb];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[db][r] *= a.scale;
-    for (int jj = 0; jj < a.R; ++jj) {
-      if (a.sel[row * a.R + jj] < 0) continue;
-      const float* po = a.part_dq + (row * a.R + jj) * D;
+        for (int r = 0; r < 16; ++r) {
+          float p = fast_exp2(fmaf(sa[qb][r], c2, nl));
+          if (need_mask) {
+            const int key = kt0 + kb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
+            p = (key < k_hi && (REMOTE || key <= s[qb])) ? p : 0.0f;
+          }
+          tmp[r] = p * (pa[qb][r] - dl[qb]);
+        }
+        dsv[qb][0] = pack8<DT>(tmp);
+        dsv[qb][1] = pack8<DT>(tmp + 8);
+      }
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const u16x8_t kt = ld_tr_operand(Ks[buf], KS, kb * 32 + t * 16, db * 32, lane);
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) acc[qb][db] = mfma32<DT>(kt, dsv[qb][t], acc[qb][db]);
+        }
+    }
+    if (it + 1 < ntiles) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    if (!valid[qb]) continue;
+    const int64_t row = (int64_t)s[qb] * a.Hq + h[qb];
+    if constexpr (REMOTE) {
+      float* po = a.part_dq + (int64_t)slot[qb] * D;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int d0 = db * 32 + 8 * j + 4 * hh;
           if (d0 < D) {
-            const f32x4_t o = *reinterpret_cast<const f32x4_t*>(po + d0);
+            f32x4_t o;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[db][4 * j + i] += o[i];
+            for (int i = 0; i < 4; ++i) o[i] = acc[qb][db][4 * j + i] * a.scale;
+            *reinterpret_cast<f32x4_t*>(po + d0) = o;
+          }
+        }
+    } else {
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[qb][db][r] *= a.scale;
+      for (int jj = 0; jj < a.R; ++jj) {
+        if (a.sel[row * a.R + jj] < 0) continue;
+        const float* po = a.part_dq + (row * a.R + jj) * D;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int d0 = db * 32 + 8 * j + 4 * hh;
+            if (d0 < D) {
+              const f32x4_t o = *reinterpret_cast<const f32x4_t*>(po + d0);
+#pragma unroll
+              for (int i = 0; i < 4; ++i) acc[qb][db][4 * j + i] += o[i];
+            }
+          }
+      }
+      uint16_t* orow = a.dq + row * D;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int d0 = db * 32 + 8 * j + 4 * hh;
+          if (d0 < D) {
+            u16x4_t o;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = from_f32<DT>(acc[qb][db][4 * j + i]);
+            *reinterpret_cast<u16x4_t*>(orow + d0) = o;
           }
         }
     }
-    uint16_t* orow = a.dq + row * D;
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int d0 = db * 32 + 8 * j + 4 * hh;
-        if (d0 < D) {
-          u16x4_t o;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) o[i] = from_f32<DT>(acc[db][4 * j + i]);
-          *reinterpret_cast<u16x4_t*>(orow + d0) = o;
-        }
-      }
   }
 }
 
 // ------------------------------------------------------------------- dkdv
-// DSPLIT waves share one 32-key block and split its d range (DP = 256 only),
-// so a workgroup owns 128 / DSPLIT keys.
+// One workgroup owns 128 / DSPLIT keys of one chunk and one KV head; each
+// wave holds one 32-key block of K and V as MFMA B fragments.  Query tiles of
+// 64 rows (Q and dO, row-major) are double-buffered in LDS with the next tile
+// prefetched into registers.  S = Q K^T and dP = dO V^T leave one key per lane
+// (D-layout), which is exactly the A layout of P^T / dS^T for
+// dV += P^T dO and dK += dS^T Q; dO and Q enter as B through the transposed
+// LDS read.  DSPLIT waves share a key block and split its d range (DP = 256).
 template <int DT, int DP, int DSPLIT>
 __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdArgs a) {
-  constexpr int QS = DP + 8, TS = kBQ + 8, NKS = DP / 16, NDB = DP / 32 / DSPLIT;
-  constexpr int BK = 128 / DSPLIT;
-  __shared__ __attribute__((aligned(16))) uint16_t Qs[kBQ * QS];
-  __shared__ __attribute__((aligned(16))) uint16_t Gs[kBQ * QS];
-  __shared__ __attribute__((aligned(16))) uint16_t Qt[DP * TS];
-  __shared__ __attribute__((aligned(16))) uint16_t Gt[DP * TS];
-  __shared__ float lse2s[kBQ], dels[kBQ];
-  __shared__ int qpos[kBQ];
+  constexpr int QS = DP + 8, NKS = DP / 16, NDB = DP / 32 / DSPLIT;
+  constexpr int NLD = kBQ * DP / 8 / 256;
+  __shared__ __attribute__((aligned(16))) uint16_t Qs[2][kBQ * QS];
+  __shared__ __attribute__((aligned(16))) uint16_t Gs[2][kBQ * QS];
+  __shared__ __attribute__((aligned(16))) float lse2s[2][kBQ];
+  __shared__ __attribute__((aligned(16))) float dels[2][kBQ];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int qi = lane & 31, hh = lane >> 5;
@@ -255,8 +307,9 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdArgs a) {
   const int f = a.kv_tiles[3 * blockIdx.x + 2];
   const int kh = blockIdx.y;
   const int c_lo = a.cu_chunk[c], c_hi = a.cu_chunk[c + 1];
-  const int key0 = c_lo + kt0;                 // first key of the workgroup
-  const int mykey = key0 + kblk * 32 + qi;     // this lane's key (B operand)
+  const int key0 = c_lo + kt0;              // first key of the workgroup
+  const int wkey0 = key0 + kblk * 32;       // first key of this wave
+  const int mykey = wkey0 + qi;             // this lane's key (B operand column)
   const bool key_ok = mykey < c_hi;
 
   u16x8_t kf[NKS], vf[NKS];
@@ -271,58 +324,63 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdArgs a) {
 #pragma unroll
   for (int i = 0; i < NDB; ++i) { dka[i] = zero16(); dva[i] = zero16(); }
 
-  // query tiles: G * n_self causal tiles, then the expert's rows
-  const int self_begin = key0;  // queries before the first key see none of them
-  const int n_self_rows = max(0, c_hi - self_begin);
-  const int n_self = (n_self_rows + kBQ - 1) / kBQ;
+  // query tiles: G * n_self causal tiles (rows from key0 to the chunk end, for
+  // every head of the group), then the expert's gathered rows
+  const int self_begin = key0;
+  const int n_self = (max(0, c_hi - self_begin) + kBQ - 1) / kBQ;
   const int e = (f >= 0 && a.R > 0) ? f * a.Hkv + kh : -1;
-  const int n_rem_rows = e >= 0 ? a.counts[e] : 0;
+  const int n_rem = e >= 0 ? a.counts[e] : 0;
   const int rbase = e >= 0 ? a.row_off[e] : 0;
-  const int n_tiles = G * n_self + (n_rem_rows + kBQ - 1) / kBQ;
+  const int n_tiles = G * n_self + (n_rem + kBQ - 1) / kBQ;
 
-  for (int it = 0; it < n_tiles; ++it) {
-    const bool is_self = it < G * n_self;
-    __syncthreads();
-    if (tid < kBQ) {
-      int s = 0, h = 0;
-      bool ok;
-      if (is_self) {
-        const int g = it / n_self, r0 = (it % n_self) * kBQ;
-        s = self_begin + r0 + tid;
-        h = kh * G + g;
-        ok = s < c_hi;
-      } else {
-        const int local = (it - G * n_self) * kBQ + tid;
-        ok = local < n_rem_rows;
-        if (ok) {
-          const int sh = a.rows[rbase + local] / a.R;
-          s = sh / a.Hq;
-          h = sh % a.Hq;
-        }
-      }
-      const int64_t row = (int64_t)s * a.Hq + h;
-      qpos[tid] = ok ? (int)row : -1;
-      lse2s[tid] = ok ? a.lse[row] * kLog2e : INFINITY;
-      dels[tid] = ok ? a.delta[row] : 0.0f;
+  auto row_of = [&](int it, int qr) -> int {  // row index s*Hq+h, or -1
+    if (it < G * n_self) {
+      const int g = it / n_self, s = self_begin + (it % n_self) * kBQ + qr;
+      return s < c_hi ? s * a.Hq + kh * G + g : -1;
     }
-    __syncthreads();
-    for (int id = tid; id < kBQ * (DP / 8); id += 256) {
-      const int qr = id / (DP / 8), dc = (id % (DP / 8)) * 8;
-      const int row = qpos[qr];
-      const bool ok = row >= 0 && dc < D;
-      const u16x8_t qv = ok ? ld8(a.q + (int64_t)row * D + dc) : zero8();
-      const u16x8_t gv = ok ? ld8(a.dout + (int64_t)row * D + dc) : zero8();
-      st8(&Qs[qr * QS + dc], qv);
-      st8(&Gs[qr * QS + dc], gv);
-      const int pos = (qr & ~15) + kperm16(qr & 15);
+    const int local = (it - G * n_self) * kBQ + qr;
+    return local < n_rem ? a.rows[rbase + local] / a.R : -1;
+  };
+
+  u16x8_t qr_[NLD], gr_[NLD];
+  float lse_r = INFINITY, del_r = 0.0f;
+  auto gload = [&](int it) {
 #pragma unroll
-      for (int ee = 0; ee < 8; ++ee) {
-        Qt[(dc + ee) * TS + pos] = qv[ee];
-        Gt[(dc + ee) * TS + pos] = gv[ee];
-      }
+    for (int i = 0; i < NLD; ++i) {
+      const int id = tid + i * 256, q = id / (DP / 8), dc = (id % (DP / 8)) * 8;
+      const int row = row_of(it, q);
+      const bool ok = row >= 0 && dc < D;
+      qr_[i] = ok ? ld8(a.q + (int64_t)row * D + dc) : zero8();
+      gr_[i] = ok ? ld8(a.dout + (int64_t)row * D + dc) : zero8();
     }
-    __syncthreads();
-    const int sq0 = is_self ? self_begin + ((it % n_self) * kBQ) : 0;
+    if (tid < kBQ) {
+      const int row = row_of(it, tid);
+      lse_r = row >= 0 ? a.lse[row] * kLog2e : INFINITY;
+      del_r = row >= 0 ? a.delta[row] : 0.0f;
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+      const int id = tid + i * 256, q = id / (DP / 8), dc = (id % (DP / 8)) * 8;
+      st8(&Qs[buf][q * QS + dc], qr_[i]);
+      st8(&Gs[buf][q * QS + dc], gr_[i]);
+    }
+    if (tid < kBQ) { lse2s[buf][tid] = lse_r; dels[buf][tid] = del_r; }
+  };
+
+  const float c2 = a.scale_log2;
+  if (n_tiles > 0) {
+    gload(0);
+    lstore(0);
+  }
+  __syncthreads();
+  for (int it = 0; it < n_tiles; ++it) {
+    const int buf = it & 1;
+    if (it + 1 < n_tiles) gload(it + 1);
+    const bool is_self = it < G * n_self;
+    const int sq0 = is_self ? self_begin + (it % n_self) * kBQ : 0;
+    const bool need_mask = (wkey0 + 32 > c_hi) || (is_self && sq0 < wkey0 + 31);
 
     u16x8_t pv[2][2], dsv[2][2];
 #pragma unroll
@@ -330,17 +388,23 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdArgs a) {
       f32x16_t sa = zero16(), pa = zero16();
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {
-        sa = mfma32<DT>(ld8(&Qs[(qb * 32 + qi) * QS + ks * 16 + hh * 8]), kf[ks], sa);
-        pa = mfma32<DT>(ld8(&Gs[(qb * 32 + qi) * QS + ks * 16 + hh * 8]), vf[ks], pa);
+        sa = mfma32<DT>(ld8(&Qs[buf][(qb * 32 + qi) * QS + ks * 16 + hh * 8]), kf[ks], sa);
+        pa = mfma32<DT>(ld8(&Gs[buf][(qb * 32 + qi) * QS + ks * 16 + hh * 8]), vf[ks], pa);
       }
       float pt[16], dt[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int ql = qb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
-        const bool ok = key_ok && (!is_self || mykey <= sq0 + ql);
-        const float p = ok ? exp2f(sa[r] * a.scale_log2 - lse2s[ql]) : 0.0f;
-        pt[r] = p;
-        dt[r] = p * (pa[r] - dels[ql]);
+      for (int j = 0; j < 4; ++j) {
+        const int qb0 = qb * 32 + 8 * j + 4 * hh;
+        const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(&lse2s[buf][qb0]);
+        const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(&dels[buf][qb0]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 4 * j + i;
+          float p = fast_exp2(fmaf(sa[r], c2, -l4[i]));
+          if (need_mask) p = (key_ok && (!is_self || mykey <= sq0 + qb0 + i)) ? p : 0.0f;
+          pt[r] = p;
+          dt[r] = p * (pa[r] - d4[i]);
+        }
       }
       pv[qb][0] = pack8<DT>(pt);
       pv[qb][1] = pack8<DT>(pt + 8);
@@ -354,11 +418,14 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdArgs a) {
       for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-          const int col = (db * 32 + qi) * TS + qb * 32 + t * 16 + hh * 8;
-          dva[i] = mfma32<DT>(pv[qb][t], ld8(&Gt[col]), dva[i]);
-          dka[i] = mfma32<DT>(dsv[qb][t], ld8(&Qt[col]), dka[i]);
+          const u16x8_t gt = ld_tr_operand(Gs[buf], QS, qb * 32 + t * 16, db * 32, lane);
+          const u16x8_t qt = ld_tr_operand(Qs[buf], QS, qb * 32 + t * 16, db * 32, lane);
+          dva[i] = mfma32<DT>(pv[qb][t], gt, dva[i]);
+          dka[i] = mfma32<DT>(dsv[qb][t], qt, dka[i]);
         }
     }
+    if (it + 1 < n_tiles) lstore(buf ^ 1);
+    __syncthreads();
   }
 
   // dK/dV D-layout: lane holds column d = db*32 + qi, keys 8j + 4hh + i.
@@ -368,7 +435,7 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdArgs a) {
     if (d >= D) continue;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int key = key0 + kblk * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
+      const int key = wkey0 + 8 * (r >> 2) + 4 * hh + (r & 3);
       if (key < c_hi) {
         const int64_t off = ((int64_t)key * a.Hkv + kh) * D + d;
         a.dk[off] = from_f32<DT>(dka[i][r] * a.scale);
@@ -384,9 +451,9 @@ int launch_bwd(const BwdArgs& a, int n_self, int n_kv, int max_remote, hipStream
   hipLaunchKernelGGL(delta_kernel<DT>, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, st,
                      a.out, a.dout, rows, a.D, a.delta);
   if (max_remote > 0 && a.R > 0)
-    hipLaunchKernelGGL((dq_kernel<DT, DP, true>), dim3(max_remote), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((dq_kernel<DT, DP, true, DP <= 128 ? 2 : 1>), dim3(max_remote), dim3(256), 0, st, a);
   if (n_self > 0)
-    hipLaunchKernelGGL((dq_kernel<DT, DP, false>), dim3(n_self, a.Hq), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((dq_kernel<DT, DP, false, DP <= 128 ? 2 : 1>), dim3(n_self, a.Hq), dim3(256), 0, st, a);
   if (n_kv > 0) {
     if constexpr (DP > 128)
       hipLaunchKernelGGL((dkdv_kernel<DT, DP, 2>), dim3(n_kv, a.Hkv), dim3(256), 0, st, a);

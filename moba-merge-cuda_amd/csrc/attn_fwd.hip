@@ -7,22 +7,24 @@
 // src/moba_opt/ops/merge.cu:27-153.
 //
 // Two launches, no atomics, no packed copies of Q or K/V:
-//  * remote_kernel: one workgroup per tile of <=128 rows of one expert
+//  * remote_kernel: one workgroup per tile of <=256 rows of one expert
 //    (filtered chunk, kv head).  Rows are read in place from q[T,Hq,D] through
 //    the expert's row list; the chunk's K/V tiles are staged in LDS once per
 //    workgroup.  Each row writes a normalised partial (o, lse) into its slot
 //    (s*Hq + h)*R + j, j = rank of the chunk in the row's ascending selection.
-//  * self_kernel: one workgroup per (chunk, q head, 128 consecutive rows),
+//  * self_kernel: one workgroup per (chunk, q head, 256 consecutive rows),
 //    causal within the chunk; its epilogue merges the row's partials in
 //    ascending-slot order (global softmax: m = max l, O = sum e^{l-m} o / z,
 //    L = m + log z) and writes the final O (input dtype) and LSE (fp32).
 //
-// Tile math (per wave: 32 query rows, key tiles of 64):
+// Tile math (per wave: 2 blocks of 32 query rows, key tiles of 64):
 //   S^T = K Q^T      (A = K rows from LDS, B = Q fragment in registers)
-//   O^T += V^T P^T   (A = V^T from a transposed LDS tile, B = P from the S^T
-//                     accumulators: the D-layout of S^T already is the B-layout
-//                     of P^T up to a fixed key permutation, applied when V^T is
-//                     written to LDS)
+//   O^T += V^T P^T   (A = V^T read from the row-major V tile with the gfx950
+//                     transposed LDS read, B = P straight from the S^T
+//                     accumulators: the D-layout of S^T is the B-layout of P^T
+//                     up to a fixed key order, which the transposed read follows)
+// Each K / V^T fragment read from LDS feeds the MFMAs of both query blocks, and
+// the next K/V tile is prefetched into registers while the current one computes.
 // so every per-query quantity (running max, sum, rescale) is lane-uniform.
 #include "common.h"
 #include "../../include/moba_hip.h"
@@ -53,24 +55,25 @@ struct FwdArgs {
   float* lse;
 };
 
-constexpr int kBM = 128;
-constexpr int kBN = 64;
+constexpr int kBN = 64;   // keys per LDS tile
+constexpr float kRescaleSlack = 8.0f;  // log2 headroom before O is rescaled
 
-template <int DT, int DP, bool REMOTE>
+template <int DT, int DP, bool REMOTE, int QB>
 __global__ __launch_bounds__(256, 1) void fwd_kernel(FwdArgs a) {
-  constexpr int KS = DP + 8;   // K row stride (elements) in LDS
-  constexpr int VS = kBN + 8;  // V^T row stride
-  constexpr int NKS = DP / 16; // k-steps of the QK^T contraction
-  constexpr int NDB = DP / 32; // 32-row d blocks of O^T
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[kBN * KS];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[DP * VS];
+  constexpr int KS = DP + 8;    // row stride (elements) of the K and V tiles
+  constexpr int NKS = DP / 16;  // k-steps of the QK^T contraction
+  constexpr int NDB = DP / 32;  // 32-row d blocks of O^T
+  constexpr int NLD = kBN * DP / 8 / 256;  // 16-byte chunks per thread per operand
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kBN * KS];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][kBN * KS];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int qi = lane & 31, hh = lane >> 5;
   const int D = a.D;
 
-  int s, h, kh, k_lo, k_hi, slot = 0;
-  bool valid;
+  int s[QB], h[QB], slot[QB];
+  bool valid[QB];
+  int kh, k_lo, k_hi, s_wave0 = 0;
   if constexpr (REMOTE) {
     const int t = blockIdx.x;
     if (t >= a.tile_off[a.E]) return;
@@ -84,191 +87,238 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(FwdArgs a) {
     const int c = a.filtered[e / a.Hkv];
     k_lo = a.cu_chunk[c];
     k_hi = a.cu_chunk[c + 1];
-    const int local = (t - a.tile_off[e]) * kBM + wave * 32 + qi;
-    valid = local < a.counts[e];
-    slot = valid ? a.rows[a.row_off[e] + local] : 0;
-    const int sh = slot / a.R;
-    s = sh / a.Hq;
-    h = sh % a.Hq;
+    const int cnt = a.counts[e], base = a.row_off[e];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const int local = (t - a.tile_off[e]) * (128 * QB) + wave * (32 * QB) + qb * 32 + qi;
+      valid[qb] = local < cnt;
+      slot[qb] = valid[qb] ? a.rows[base + local] : 0;
+      const int sh = slot[qb] / a.R;
+      s[qb] = sh / a.Hq;
+      h[qb] = sh % a.Hq;
+    }
   } else {
     const int c = a.self_tiles[2 * blockIdx.x], row0 = a.self_tiles[2 * blockIdx.x + 1];
-    h = blockIdx.y;
-    kh = h / a.G;
+    kh = blockIdx.y / a.G;
     k_lo = a.cu_chunk[c];
     const int c_end = a.cu_chunk[c + 1];
-    k_hi = min(c_end, k_lo + row0 + kBM);
-    s = k_lo + row0 + wave * 32 + qi;
-    valid = s < c_end;
-    if (!valid) s = k_hi - 1;
+    k_hi = min(c_end, k_lo + row0 + 128 * QB);
+    s_wave0 = k_lo + row0 + wave * (32 * QB);
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      h[qb] = blockIdx.y;
+      s[qb] = s_wave0 + qb * 32 + qi;
+      valid[qb] = s[qb] < c_end;
+      if (!valid[qb]) s[qb] = k_hi - 1;
+    }
   }
 
-  const int64_t qrow = ((int64_t)s * a.Hq + h) * D;
-  u16x8_t qf[NKS];
+  u16x8_t qf[QB][NKS];
 #pragma unroll
-  for (int ks = 0; ks < NKS; ++ks) {
-    const int d = ks * 16 + hh * 8;
-    qf[ks] = (valid && d < D) ? ld8(a.q + qrow + d) : zero8();
+  for (int qb = 0; qb < QB; ++qb) {
+    const int64_t qrow = ((int64_t)s[qb] * a.Hq + h[qb]) * D;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const int d = ks * 16 + hh * 8;
+      qf[qb][ks] = (valid[qb] && d < D) ? ld8(a.q + qrow + d) : zero8();
+    }
   }
 
-  f32x16_t oacc[NDB];
+  u16x8_t kr[NLD], vr[NLD];
+  auto gload = [&](int kt0) {
 #pragma unroll
-  for (int db = 0; db < NDB; ++db) oacc[db] = zero16();
-  float m_run = -INFINITY, lsum = 0.0f;
-
-  for (int kt0 = k_lo; kt0 < k_hi; kt0 += kBN) {
-    __syncthreads();
-    for (int id = tid; id < kBN * (DP / 8); id += 256) {
-      const int key = id / (DP / 8), dc = (id % (DP / 8)) * 8;
+    for (int i = 0; i < NLD; ++i) {
+      const int id = tid + i * 256, key = id / (DP / 8), dc = (id % (DP / 8)) * 8;
       const int kg = kt0 + key;
       const bool ok = kg < k_hi && dc < D;
       const int64_t off = ((int64_t)kg * a.Hkv + kh) * D + dc;
-      const u16x8_t kv = ok ? ld8(a.k + off) : zero8();
-      const u16x8_t vv = ok ? ld8(a.v + off) : zero8();
-      st8(&Ks[key * KS + dc], kv);
-      const int pos = (key & ~15) + kperm16(key & 15);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) Vt[(dc + e) * VS + pos] = vv[e];
+      kr[i] = ok ? ld8(a.k + off) : zero8();
+      vr[i] = ok ? ld8(a.v + off) : zero8();
     }
-    __syncthreads();
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+      const int id = tid + i * 256, key = id / (DP / 8), dc = (id % (DP / 8)) * 8;
+      st8(&Ks[buf][key * KS + dc], kr[i]);
+      st8(&Vs[buf][key * KS + dc], vr[i]);
+    }
+  };
 
-    f32x16_t sacc[2];
+  f32x16_t oacc[QB][NDB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) oacc[qb][db] = zero16();
+  float m_run[QB], lsum[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) { m_run[qb] = -INFINITY; lsum[qb] = 0.0f; }
+  const float c2 = a.scale_log2;
+
+  const int ntiles = (k_hi - k_lo + kBN - 1) / kBN;
+  gload(k_lo);
+  lstore(0);
+  __syncthreads();
+  for (int it = 0; it < ntiles; ++it) {
+    const int kt0 = k_lo + it * kBN, buf = it & 1;
+    if (it + 1 < ntiles) gload(kt0 + kBN);
+
+    f32x16_t sacc[QB][2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      sacc[kb] = zero16();
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) sacc[qb][kb] = zero16();
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {
-        const u16x8_t av = ld8(&Ks[(kb * 32 + qi) * KS + ks * 16 + hh * 8]);
-        sacc[kb] = mfma32<DT>(av, qf[ks], sacc[kb]);
+        const u16x8_t av = ld8(&Ks[buf][(kb * 32 + qi) * KS + ks * 16 + hh * 8]);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) sacc[qb][kb] = mfma32<DT>(av, qf[qb][ks], sacc[qb][kb]);
       }
     }
-    float mloc = -INFINITY;
+    const bool need_mask = (kt0 + kBN > k_hi) || (!REMOTE && kt0 + kBN - 1 > s_wave0);
+    if (need_mask) {
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+      for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kt0 + kb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
-        const bool ok = key < k_hi && (REMOTE || key <= s);
-        const float x = ok ? sacc[kb][r] * a.scale_log2 : -INFINITY;
-        sacc[kb][r] = x;
-        mloc = fmaxf(mloc, x);
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = kt0 + kb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
+            const bool ok = key < k_hi && (REMOTE || key <= s[qb]);
+            sacc[qb][kb][r] = ok ? sacc[qb][kb][r] : -INFINITY;
+          }
+    }
+    u16x8_t pv[QB][2][2];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[qb][kb][r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c2;
+      // Lazy rescale: keep the running max while the new scores stay within
+      // 2^8 of it (p <= 256 is exact enough in bf16/fp32); O, l and the final
+      // normalisation all use the same reference so the result is unchanged.
+      const bool up = mx > m_run[qb] + kRescaleSlack;
+      if (__any(up)) {
+        const float mn = up ? mx : m_run[qb];
+        const float alpha = fast_exp2(m_run[qb] - mn);
+        lsum[qb] *= alpha;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[qb][db][r] *= alpha;
+        m_run[qb] = mn;
       }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-    const float m_new = fmaxf(m_run, mloc);
-    const float alpha = exp2f(m_run - m_new);
-    float ps = 0.0f;
+      const float nm = -m_run[qb];
+      float ps = 0.0f;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < 2; ++kb) {
+        float p[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = exp2f(sacc[kb][r] - m_new);
-        sacc[kb][r] = p;
-        ps += p;
+        for (int r = 0; r < 16; ++r) {
+          p[r] = fast_exp2(fmaf(sacc[qb][kb][r], c2, nm));
+          ps += p[r];
+        }
+        pv[qb][kb][0] = pack8<DT>(p);
+        pv[qb][kb][1] = pack8<DT>(p + 8);
       }
-    lsum = lsum * alpha + ps;
-    m_run = m_new;
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
-
-    u16x8_t pv[2][2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        float tmp[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) tmp[e] = sacc[kb][8 * t + e];
-        pv[kb][t] = pack8<DT>(tmp);
-      }
+      lsum[qb] += ps;
+    }
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-          const u16x8_t av = ld8(&Vt[(db * 32 + qi) * VS + kb * 32 + t * 16 + hh * 8]);
-          oacc[db] = mfma32<DT>(av, pv[kb][t], oacc[db]);
+          const u16x8_t av = ld_tr_operand(Vs[buf], KS, kb * 32 + t * 16, db * 32, lane);
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) oacc[qb][db] = mfma32<DT>(av, pv[qb][kb][t], oacc[qb][db]);
         }
+    if (it + 1 < ntiles) lstore(buf ^ 1);
+    __syncthreads();
   }
 
-  const float l = lsum + __shfl_xor(lsum, 32, 64);
-  const float L2 = m_run + log2f(l);
-  if (!valid) return;
-
-  if constexpr (REMOTE) {
-    const float inv = 1.0f / l;
-    float* po = a.part_o + (int64_t)slot * D;
 #pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int d0 = db * 32 + 8 * j + 4 * hh;
-        if (d0 < D) {
-          f32x4_t o;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) o[i] = oacc[db][4 * j + i] * inv;
-          *reinterpret_cast<f32x4_t*>(po + d0) = o;
-        }
-      }
-    if (hh == 0) a.part_lse[slot] = L2 * kLn2;
-  } else {
-    const int64_t row = (int64_t)s * a.Hq + h;
-    float M2 = L2;
-    for (int jj = 0; jj < a.R; ++jj)
-      if (a.sel[row * a.R + jj] >= 0) M2 = fmaxf(M2, a.part_lse[row * a.R + jj] * kLog2e);
-    const float ws = exp2f(L2 - M2);
-    float z = ws;
-    const float cs = ws / l;
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) oacc[db][r] *= cs;
-    for (int jj = 0; jj < a.R; ++jj) {
-      if (a.sel[row * a.R + jj] < 0) continue;
-      const int64_t sl = row * a.R + jj;
-      const float w = exp2f(a.part_lse[sl] * kLog2e - M2);
-      z += w;
-      const float* po = a.part_o + sl * D;
+  for (int qb = 0; qb < QB; ++qb) {
+    const float l = lsum[qb] + __shfl_xor(lsum[qb], 32, 64);
+    const float L2 = m_run[qb] + log2f(l);
+    if (!valid[qb]) continue;
+    if constexpr (REMOTE) {
+      const float inv = 1.0f / l;
+      float* po = a.part_o + (int64_t)slot[qb] * D;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int d0 = db * 32 + 8 * j + 4 * hh;
           if (d0 < D) {
-            const f32x4_t o = *reinterpret_cast<const f32x4_t*>(po + d0);
+            f32x4_t o;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) oacc[db][4 * j + i] += w * o[i];
+            for (int i = 0; i < 4; ++i) o[i] = oacc[qb][db][4 * j + i] * inv;
+            *reinterpret_cast<f32x4_t*>(po + d0) = o;
           }
         }
-    }
-    const float invz = 1.0f / z;
-    uint16_t* orow = a.out + row * D;
+      if (hh == 0) a.part_lse[slot[qb]] = L2 * kLn2;
+    } else {
+      const int64_t row = (int64_t)s[qb] * a.Hq + h[qb];
+      float M2 = L2;
+      for (int jj = 0; jj < a.R; ++jj)
+        if (a.sel[row * a.R + jj] >= 0) M2 = fmaxf(M2, a.part_lse[row * a.R + jj] * kLog2e);
+      const float ws = exp2f(L2 - M2);
+      float z = ws;
+      const float cs = ws / l;
 #pragma unroll
-    for (int db = 0; db < NDB; ++db)
+      for (int db = 0; db < NDB; ++db)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int d0 = db * 32 + 8 * j + 4 * hh;
-        if (d0 < D) {
-          u16x4_t o;
+        for (int r = 0; r < 16; ++r) oacc[qb][db][r] *= cs;
+      for (int jj = 0; jj < a.R; ++jj) {
+        if (a.sel[row * a.R + jj] < 0) continue;
+        const int64_t sl = row * a.R + jj;
+        const float w = exp2f(a.part_lse[sl] * kLog2e - M2);
+        z += w;
+        const float* po = a.part_o + sl * D;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) o[i] = from_f32<DT>(oacc[db][4 * j + i] * invz);
-          *reinterpret_cast<u16x4_t*>(orow + d0) = o;
-        }
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int d0 = db * 32 + 8 * j + 4 * hh;
+            if (d0 < D) {
+              const f32x4_t o = *reinterpret_cast<const f32x4_t*>(po + d0);
+#pragma unroll
+              for (int i = 0; i < 4; ++i) oacc[qb][db][4 * j + i] += w * o[i];
+            }
+          }
       }
-    if (hh == 0) a.lse[row] = (M2 + log2f(z)) * kLn2;
+      const float invz = 1.0f / z;
+      uint16_t* orow = a.out + row * D;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int d0 = db * 32 + 8 * j + 4 * hh;
+          if (d0 < D) {
+            u16x4_t o;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = from_f32<DT>(oacc[qb][db][4 * j + i] * invz);
+            *reinterpret_cast<u16x4_t*>(orow + d0) = o;
+          }
+        }
+      if (hh == 0) a.lse[row] = (M2 + log2f(z)) * kLn2;
+    }
   }
 }
 
 template <int DT, int DP>
 int launch_fwd(const FwdArgs& a, int n_self_tiles, int max_remote_tiles, hipStream_t st) {
   if (max_remote_tiles > 0 && a.R > 0) {
-    hipLaunchKernelGGL((fwd_kernel<DT, DP, true>), dim3(max_remote_tiles), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((fwd_kernel<DT, DP, true, DP <= 128 ? 2 : 1>), dim3(max_remote_tiles), dim3(256), 0, st, a);
     int rc = moba_launch_status("prefill_fwd(remote)");
     if (rc) return rc;
   }
   if (n_self_tiles > 0) {
-    hipLaunchKernelGGL((fwd_kernel<DT, DP, false>), dim3(n_self_tiles, a.Hq), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((fwd_kernel<DT, DP, false, DP <= 128 ? 2 : 1>), dim3(n_self_tiles, a.Hq), dim3(256), 0, st, a);
     return moba_launch_status("prefill_fwd(self)");
   }
   return MOBA_OK;

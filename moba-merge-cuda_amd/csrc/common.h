@@ -45,8 +45,11 @@ MOBA_DEV uint16_t f32_to_f16(float f) {
 template <int DT> MOBA_DEV float to_f32(uint16_t v) {
   if constexpr (DT == 0) return bf16_to_f32(v); else return f16_to_f32(v);
 }
+// Hardware conversion (v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32, round to nearest
+// even; identical to f32_to_bf16 for every non-NaN input).
 template <int DT> MOBA_DEV uint16_t from_f32(float v) {
-  if constexpr (DT == 0) return f32_to_bf16(v); else return f32_to_f16(v);
+  if constexpr (DT == 0) return __builtin_bit_cast(uint16_t, (__bf16)v);
+  else return f32_to_f16(v);
 }
 
 // 32x32x16 MFMA on 8 packed 16-bit elements per lane.
@@ -83,6 +86,34 @@ MOBA_DEV void st8(uint16_t* p, const u16x8_t& v) { *reinterpret_cast<u16x8_t*>(p
 // {4h..4h+3, 8+4h..8+4h+3} of each 16-key group; storing key r at this
 // position makes those 8 keys contiguous at offset 8h.
 MOBA_DEV int kperm16(int r) { return ((r >> 2) & 1) * 8 + ((r >> 3) & 1) * 4 + (r & 3); }
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+
+// gfx950 transposed LDS read (ds_read_b64_tr_b16).  In each 16-lane group,
+// lane i receives column (cbase + i) of 4 consecutive rows k0..k0+3 of a
+// row-major LDS tile when lane i' of the group addresses
+// row k0 + i'/4, columns cbase + 4*(i'%4) .. +3.
+MOBA_DEV u16x4_t ld_tr4(const uint16_t* p) {
+  s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(p));
+  return __builtin_bit_cast(u16x4_t, v);
+}
+
+// MFMA 32x32x16 operand whose contraction index runs over ROWS of a row-major
+// LDS tile X (stride ld elements): lane (col = l%32, half hh) gets
+// X[g16 + 4hh + 0..3][c0 + l%32] and X[g16 + 8 + 4hh + 0..3][c0 + l%32], i.e.
+// the same key order as the P/dS operands built from a D-layout accumulator.
+MOBA_DEV u16x8_t ld_tr_operand(const uint16_t* X, int ld, int g16, int c0, int lane) {
+  const int hh = lane >> 5, sub = lane & 15, cb = c0 + ((lane >> 4) & 1) * 16;
+  const uint16_t* p0 = X + (g16 + 4 * hh + (sub >> 2)) * ld + cb + 4 * (sub & 3);
+  const u16x4_t a = ld_tr4(p0), b = ld_tr4(p0 + 8 * ld);
+  u16x8_t r;
+  r[0] = a[0]; r[1] = a[1]; r[2] = a[2]; r[3] = a[3];
+  r[4] = b[0]; r[5] = b[1]; r[6] = b[2]; r[7] = b[3];
+  return r;
+}
+
+MOBA_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 template <int DT> MOBA_DEV u16x8_t pack8(const float* v) {
   u16x8_t r;

@@ -14,7 +14,6 @@ import torch
 
 from . import _lib
 
-BLOCK_ROWS = 128  # query rows per attention workgroup (4 waves x 32)
 DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1}
 
 
@@ -27,6 +26,9 @@ class PrefillPlan:
         self.chunk = chunk
         self.hq, self.hkv = hq, hkv
         self.groups = hq // hkv
+        # query rows per attention workgroup: 4 waves x (2 or 1) blocks x 32
+        self.block_rows = 256 if head_dim <= 128 else 128
+        BLOCK_ROWS = self.block_rows
         cu_chunk, chunk_batch, filtered = [0], [], []
         for b in range(len(cu) - 1):
             length = cu[b + 1] - cu[b]
@@ -139,7 +141,7 @@ def route(plan: PrefillPlan, q, k, precision: int, want_gate=False):
               _lib.ptr(gate), st)
     _lib.call("moba_hip_pack_experts", r.sel.data_ptr(), T, hq, plan.hkv, R,
               plan.ptr("cu_chunk"), plan.ptr("chunk_batch"), plan.ptr("cu_seqlens"),
-              plan.ptr("filtered"), F, BLOCK_ROWS, r.counts.data_ptr(), r.row_off.data_ptr(),
+              plan.ptr("filtered"), F, plan.block_rows, r.counts.data_ptr(), r.row_off.data_ptr(),
               r.tile_off.data_ptr(), r.rows.data_ptr(), st)
     return (r, gate) if want_gate else r
 
