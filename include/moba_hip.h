@@ -75,13 +75,14 @@ int moba_hip_pack_experts(const int* sel, int T, int Hq, int Hkv, int R,
  * tiles of 256 rows (128 when D > 128); sel/R, filtered[F] and the pack_experts outputs describe
  * the remote rows (R = 0: self branch only, e.g. the full-causal fallback with
  * one chunk per sequence).  max_remote_tiles bounds tile_off[E].
- * part_o [T*Hq*R, D] fp32 and part_lse [T*Hq*R] are workspaces.
+ * part_o [T*Hq*R, D] fp32 and part_ml [T*Hq*R, 2] fp32 (per-slot softmax
+ * max and sum in the log2 domain) are workspaces.
  * out [T,Hq,D] (dtype), lse [T,Hq] fp32 natural-log global LSE. */
 int moba_hip_prefill_fwd(const void* q, const void* k, const void* v, int dtype, int T, int Hq,
                          int Hkv, int D, float scale, const int* cu_chunk, const int* self_tiles,
                          int n_self_tiles, const int* sel, int R, const int* filtered, int E,
                          const int* tile_off, const int* row_off, const int* counts,
-                         const int* rows, int max_remote_tiles, float* part_o, float* part_lse,
+                         const int* rows, int max_remote_tiles, float* part_o, float* part_ml,
                          void* out, float* lse, void* stream);
 
 /* Backward of moba_hip_prefill_fwd with the GLOBAL O and LSE.
@@ -101,6 +102,65 @@ int moba_hip_prefill_bwd(const void* q, const void* k, const void* v, const void
                          const int* row_off, const int* counts, const int* rows,
                          int max_remote_tiles, float* delta, float* part_dq, void* dq, void* dk,
                          void* dv, void* stream);
+
+/* ----------------------------------------------------------------- decode */
+
+/* Tokens per paged_attention work item (sizes the split-K partial buffers). */
+int moba_hip_decode_sub_tokens(void);
+
+/* Scatter N new tokens k/v [N,Hkv,D] into the page pool
+ * k_cache/v_cache [num_pages, page_size, Hkv, D] at (token_seq[n], token_pos[n])
+ * through table [B, table_width] (physical page per logical page).
+ * Replaces _append_kernel (src/moba_opt/ops/paged_decode.py:10-23). */
+int moba_hip_paged_append(const void* k, const void* v, int dtype, int N, int Hkv, int D,
+                          void* k_cache, void* v_cache, int page_size, const int* table,
+                          int table_width, const int* token_seq, const int* token_pos,
+                          void* stream);
+
+/* Key means of closed chunks into means [B, max_chunks, Hkv, D] (cache dtype),
+ * fp32 sequential sum / chunk.  mode 0: item i = (item_seq[i], chunk
+ * item_chunk_or_pos[i]); mode 1: item i = query row at position p, closing
+ * chunk p / chunk only when (p + 1) % chunk == 0.
+ * Replaces _closed_means_kernel (paged_decode.py:26-44) and _step_means
+ * (src/moba_opt/ops/prepared_decode.py:23-41). */
+int moba_hip_block_means(const void* k_cache, int dtype, int Hkv, int D, int page_size,
+                         const int* table, int table_width, const int* item_seq,
+                         const int* item_chunk_or_pos, int n_items, int mode, int chunk,
+                         void* means, int max_chunks, void* stream);
+
+/* Route of decode queries q [Nq,Hq,D]: fp32 fma-chain scores against the means
+ * of the closed chunks c with (c+1)*chunk <= pos, stable top-R (descending,
+ * ties -> lowest chunk).  selected [Nq,Hq,1+R]: slot 0 = pos / chunk, then the
+ * chosen chunks, -1 padded.  scores (nullable) [Nq,Hq,width].
+ * Replaces _route_kernel + torch.topk / _stable_topk + _selected
+ * (paged_decode.py:47-64, src/moba_opt/kv_cache.py:208-223,
+ * prepared_decode.py:44-88). */
+int moba_hip_decode_route(const void* q, int dtype, int Nq, int Hq, int Hkv, int D,
+                          const void* means, int max_chunks, const int* q_seq, const int* q_pos,
+                          int chunk, int width, int R, float* scores, int* selected,
+                          void* stream);
+
+/* Paged attention of q [Nq,Hq,D] over the selected chunks (selected
+ * [Nq,Hq,nslot]) or, with dense != 0, over every token <= pos; tokens are read
+ * through the page table, each selected page once per KV-head group.
+ * max_chunks_bound (dense) bounds pos / chunk + 1.  part_o
+ * [Nq*Hq*S*nsub, D] and part_ml [Nq*Hq*S*nsub, 2] (S = nslot, or
+ * max_chunks_bound when dense; nsub = ceil(chunk / moba_hip_decode_sub_tokens()))
+ * are workspaces.  out [Nq,Hq,D] (dtype), lse [Nq,Hq] fp32 natural log.
+ * Replaces _attention_kernel (paged_decode.py:67-112). */
+int moba_hip_paged_attention(const void* q, int dtype, int Nq, int Hq, int Hkv, int D,
+                             const void* k_cache, const void* v_cache, int page_size,
+                             const int* table, int table_width, const int* lengths,
+                             const int* q_seq, const int* q_pos, const int* selected, int nslot,
+                             int dense, int chunk, int max_chunks_bound, float* part_o,
+                             float* part_ml, void* out, float* lse, void* stream);
+
+/* Prepared-decode metadata step for B fixed rows: apply the page-table delta
+ * [2,B] (logical, physical; -1 = none), write positions = lengths (append) or
+ * lengths - 1, and advance lengths when append != 0.
+ * Replaces _metadata (prepared_decode.py:6-20). */
+int moba_hip_decode_metadata(int* table, int table_width, int* lengths, const int* ids,
+                             int* positions, const int* delta, int B, int append, void* stream);
 
 #ifdef __cplusplus
 }

@@ -10,7 +10,8 @@
 //  * remote_kernel: one workgroup per tile of <=256 rows of one expert
 //    (filtered chunk, kv head).  Rows are read in place from q[T,Hq,D] through
 //    the expert's row list; the chunk's K/V tiles are staged in LDS once per
-//    workgroup.  Each row writes a normalised partial (o, lse) into its slot
+//    workgroup.  Each row writes a normalised partial o and its (max, sum)
+//    softmax statistics into its slot
 //    (s*Hq + h)*R + j, j = rank of the chunk in the row's ascending selection.
 //  * self_kernel: one workgroup per (chunk, q head, 256 consecutive rows),
 //    causal within the chunk; its epilogue merges the row's partials in
@@ -50,7 +51,7 @@ struct FwdArgs {
   const int* counts;
   const int* rows;
   float* part_o;
-  float* part_lse;
+  float* part_ml;
   uint16_t* out;
   float* lse;
 };
@@ -243,7 +244,6 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(FwdArgs a) {
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     const float l = lsum[qb] + __shfl_xor(lsum[qb], 32, 64);
-    const float L2 = m_run[qb] + log2f(l);
     if (!valid[qb]) continue;
     if constexpr (REMOTE) {
       const float inv = 1.0f / l;
@@ -260,23 +260,28 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(FwdArgs a) {
             *reinterpret_cast<f32x4_t*>(po + d0) = o;
           }
         }
-      if (hh == 0) a.part_lse[slot[qb]] = L2 * kLn2;
+      // partial stored as (running max, sum) in the log2 domain: merging
+      // them is exact in fp32 even when |logits| is huge (an LSE would round
+      // log2(l) away next to a large max)
+      if (hh == 0) {
+        a.part_ml[2 * (int64_t)slot[qb]] = m_run[qb];
+        a.part_ml[2 * (int64_t)slot[qb] + 1] = l;
+      }
     } else {
       const int64_t row = (int64_t)s[qb] * a.Hq + h[qb];
-      float M2 = L2;
+      float M2 = m_run[qb];
       for (int jj = 0; jj < a.R; ++jj)
-        if (a.sel[row * a.R + jj] >= 0) M2 = fmaxf(M2, a.part_lse[row * a.R + jj] * kLog2e);
-      const float ws = exp2f(L2 - M2);
-      float z = ws;
-      const float cs = ws / l;
+        if (a.sel[row * a.R + jj] >= 0) M2 = fmaxf(M2, a.part_ml[2 * (row * a.R + jj)]);
+      const float ws = fast_exp2(m_run[qb] - M2);
+      float z = l * ws;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[qb][db][r] *= cs;
+        for (int r = 0; r < 16; ++r) oacc[qb][db][r] *= ws;
       for (int jj = 0; jj < a.R; ++jj) {
         if (a.sel[row * a.R + jj] < 0) continue;
         const int64_t sl = row * a.R + jj;
-        const float w = exp2f(a.part_lse[sl] * kLog2e - M2);
+        const float w = a.part_ml[2 * sl + 1] * fast_exp2(a.part_ml[2 * sl] - M2);
         z += w;
         const float* po = a.part_o + sl * D;
 #pragma unroll
@@ -339,7 +344,7 @@ extern "C" int moba_hip_prefill_fwd(const void* q, const void* k, const void* v,
                                     const int* self_tiles, int n_self_tiles, const int* sel, int R,
                                     const int* filtered, int E, const int* tile_off,
                                     const int* row_off, const int* counts, const int* rows,
-                                    int max_remote_tiles, float* part_o, float* part_lse,
+                                    int max_remote_tiles, float* part_o, float* part_ml,
                                     void* out, float* lse, void* stream) {
   if (dtype != 0 && dtype != 1) { moba_set_error("prefill_fwd: dtype must be 0 (bf16) or 1 (fp16)"); return MOBA_ERR_ARG; }
   if (D < 8 || D > 256 || D % 8) { moba_set_error("prefill_fwd: head_dim must be a multiple of 8 in [8,256]"); return MOBA_ERR_ARG; }
@@ -353,7 +358,7 @@ extern "C" int moba_hip_prefill_fwd(const void* q, const void* k, const void* v,
   a.cu_chunk = cu_chunk; a.self_tiles = self_tiles;
   a.sel = sel; a.R = R; a.filtered = filtered; a.E = E;
   a.tile_off = tile_off; a.row_off = row_off; a.counts = counts; a.rows = rows;
-  a.part_o = part_o; a.part_lse = part_lse;
+  a.part_o = part_o; a.part_ml = part_ml;
   a.out = (uint16_t*)out; a.lse = lse;
   hipStream_t st = (hipStream_t)stream;
   return dtype == 0 ? dispatch_fwd<0>(a, n_self_tiles, R > 0 ? max_remote_tiles : 0, st)

@@ -1,0 +1,65 @@
+"""Launch wrappers of the decode entry points of libmoba_hip.so."""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1}
+
+
+def sub_tokens() -> int:
+    return _lib.load().moba_hip_decode_sub_tokens()
+
+
+def append_tokens(k, v, kc, vc, table, token_seq, token_pos):
+    n, hk, d = k.shape
+    _lib.call("moba_hip_paged_append", k.data_ptr(), v.data_ptr(), DTYPE_CODE[k.dtype], n, hk, d,
+              kc.data_ptr(), vc.data_ptr(), kc.shape[1], table.data_ptr(), table.shape[1],
+              token_seq.data_ptr(), token_pos.data_ptr(), _lib.stream_of(k.device))
+
+
+def block_means(kc, table, means, item_seq, item_chunk_or_pos, chunk, mode=0):
+    n = item_seq.numel()
+    if n == 0:
+        return
+    hk, d = kc.shape[2:]
+    _lib.call("moba_hip_block_means", kc.data_ptr(), DTYPE_CODE[kc.dtype], hk, d, kc.shape[1],
+              table.data_ptr(), table.shape[1], item_seq.data_ptr(), item_chunk_or_pos.data_ptr(),
+              n, mode, chunk, means.data_ptr(), means.shape[1], _lib.stream_of(kc.device))
+
+
+def route(q, means, q_seq, q_pos, chunk, width, remote, scores, selected):
+    nq, hq, d = q.shape
+    _lib.call("moba_hip_decode_route", q.data_ptr(), DTYPE_CODE[q.dtype], nq, hq, means.shape[2],
+              d, means.data_ptr(), means.shape[1], q_seq.data_ptr(), q_pos.data_ptr(), chunk,
+              width, remote, _lib.ptr(scores), selected.data_ptr(), _lib.stream_of(q.device))
+
+
+def workspace_entries(nq, hq, nslot, chunk):
+    nsub = -(-chunk // sub_tokens())
+    return nq * hq * nslot * nsub
+
+
+def attention(q, kc, vc, table, lengths, q_seq, q_pos, selected, out, lse, chunk, dense,
+              max_chunks_bound, part_o=None, part_ml=None):
+    """Paged MoBA / dense attention.  ``selected`` [Nq,Hq,nslot] (ignored when
+    dense); workspaces are allocated here unless given (graph capture)."""
+    nq, hq, d = q.shape
+    nslot = max_chunks_bound if dense else selected.shape[-1]
+    if part_o is None:
+        n = workspace_entries(nq, hq, nslot, chunk)
+        part_o = torch.empty((n, d), dtype=torch.float32, device=q.device)
+        part_ml = torch.empty((n, 2), dtype=torch.float32, device=q.device)
+    _lib.call("moba_hip_paged_attention", q.data_ptr(), DTYPE_CODE[q.dtype], nq, hq, kc.shape[2],
+              d, kc.data_ptr(), vc.data_ptr(), kc.shape[1], table.data_ptr(), table.shape[1],
+              lengths.data_ptr(), q_seq.data_ptr(), q_pos.data_ptr(),
+              None if dense else selected.data_ptr(), 0 if dense else nslot, 1 if dense else 0,
+              chunk, max_chunks_bound, part_o.data_ptr(), part_ml.data_ptr(), out.data_ptr(),
+              lse.data_ptr(), _lib.stream_of(q.device))
+
+
+def metadata(table, lengths, ids, positions, delta, append):
+    _lib.call("moba_hip_decode_metadata", table.data_ptr(), table.shape[1], lengths.data_ptr(),
+              ids.data_ptr(), positions.data_ptr(), delta.data_ptr(), ids.numel(),
+              1 if append else 0, _lib.stream_of(table.device))

@@ -153,17 +153,17 @@ def forward(plan: PrefillPlan, q, k, v, rt: RouteResult | None):
     R = plan.remote
     out = torch.empty_like(q)
     lse = torch.empty((T, hq), dtype=torch.float32, device=dev)
-    part_o = part_lse = None
+    part_o = part_ml = None
     if R:
         part_o = torch.empty((T * hq * R, d), dtype=torch.float32, device=dev)
-        part_lse = torch.empty(T * hq * R, dtype=torch.float32, device=dev)
+        part_ml = torch.empty((T * hq * R, 2), dtype=torch.float32, device=dev)
     _lib.call("moba_hip_prefill_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(),
               DTYPE_CODE[q.dtype], T, hq, plan.hkv, d, d ** -0.5,
               plan.ptr("att_chunk"), plan.ptr("self_tiles"), plan.n_self_tiles,
               _lib.ptr(rt.sel) if R else None, R, plan.ptr("filtered"), plan.num_experts,
               _lib.ptr(rt.tile_off) if R else None, _lib.ptr(rt.row_off) if R else None,
               _lib.ptr(rt.counts) if R else None, _lib.ptr(rt.rows) if R else None,
-              plan.max_remote_tiles if R else 0, _lib.ptr(part_o), _lib.ptr(part_lse),
+              plan.max_remote_tiles if R else 0, _lib.ptr(part_o), _lib.ptr(part_ml),
               out.data_ptr(), lse.data_ptr(), _lib.stream_of(dev))
     return out, lse
 

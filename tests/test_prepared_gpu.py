@@ -1,0 +1,167 @@
+"""GPU parity of PreparedDecode with and without hipGraph replay (cases follow
+tests/test_prepared_decode.py of the reference)."""
+import pytest
+import torch
+
+from decode_check import check, rand
+
+pytestmark = pytest.mark.gpu
+
+
+def _paged():
+    from moba_hip import PagedKVCache
+    return PagedKVCache
+
+
+@pytest.mark.parametrize("graph", [False, True])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("page,chunk,dim,hq,hk", [(3, 4, 33, 15, 3), (7, 6, 64, 8, 1),
+                                                   (16, 8, 128, 8, 2)])
+def test_prepared_steps_match_fp64(cuda_device, graph, dtype, page, chunk, dim, hq, hk):
+    cache = _paged()(3, 40, hk, dim, page_size=page, chunk_size=chunk, dtype=dtype)
+    k, v = rand((14, hk, dim), dtype, 501), rand((14, hk, dim), dtype, 502)
+    cache.append(k, v, sequence_ids=[2, 0], cu_seqlens=[0, 5, 14])
+    sk, sv = {2: k[:5], 0: k[5:]}, {2: v[:5], 0: v[5:]}
+    lengths, table = cache.lengths, cache.page_table
+    before = [cache.materialize(s) for s in (2, 0)]
+    with cache.prepare_decode([2, 0], hq, topk=3) as plan:
+        if graph:
+            plan.capture("step").capture("attend")
+            assert cache.lengths == lengths and cache.page_table == table
+            for sid, (bk, bv) in zip((2, 0), before):
+                ak, av = cache.materialize(sid)
+                assert torch.equal(ak, bk) and torch.equal(av, bv)
+        ptrs = [t.data_ptr() for t in (cache._table, cache._lengths, plan.output, plan.scores,
+                                       plan.selected)]
+        for step in range(10):
+            q = rand((2, hq, dim), dtype, 510 + step)
+            kn, vn = rand((2, hk, dim), dtype, 530 + step), rand((2, hk, dim), dtype, 550 + step)
+            result = plan.step(q, kn, vn, use_graph=graph)
+            for i, sid in enumerate((2, 0)):
+                sk[sid] = torch.cat((sk[sid], kn[i:i + 1]))
+                sv[sid] = torch.cat((sv[sid], vn[i:i + 1]))
+                ak, av = cache.materialize(sid)
+                assert torch.equal(ak, sk[sid]) and torch.equal(av, sv[sid])
+            check(cache, result, q)
+            check(cache, plan.attend(q, use_graph=graph), q)
+        assert ptrs == [t.data_ptr() for t in (cache._table, cache._lengths, plan.output,
+                                               plan.scores, plan.selected)]
+        assert plan.delta_uploads <= 10
+        with pytest.raises(ValueError, match="owns cache"):
+            cache.reset()
+    cache.reset([2])
+    assert cache.lengths == (19, 0, 0)
+
+
+@pytest.mark.parametrize("graph", [False, True])
+@pytest.mark.parametrize("mode,topk", [("moba", 1), ("dense", 4), ("moba", 9)])
+def test_prepared_empty_and_dense_fallback(cuda_device, graph, mode, topk):
+    cache = _paged()(1, 17, 1, 8, page_size=3, chunk_size=4)
+    with cache.prepare_decode([0], 4, topk=topk, mode=mode) as p:
+        if graph:
+            p.capture("step")
+        for step in range(9):
+            q = rand((1, 4, 8), cache.dtype, 601 + step)
+            kv = rand((1, 1, 8), cache.dtype, 621 + step)
+            check(cache, p.step(q, kv, kv, use_graph=graph), q)
+
+
+def test_lifecycle_capacity_and_metadata_delta(cuda_device):
+    c = _paged()(1, 7, 1, 8, page_size=3, chunk_size=4)
+    q = torch.ones((1, 1, 8), device="cuda", dtype=c.dtype)
+    with c.prepare_decode([0], 1) as p:
+        before = c.lengths
+        with pytest.raises(ValueError, match="NaN/Inf"):
+            p.step(q * float("nan"), q, q)
+        with pytest.raises(ValueError, match="capture"):
+            p.step(q, q, q, use_graph=True)
+        assert c.lengths == before
+        for _ in range(7):
+            p.step(q, q, q)
+        assert p.delta_uploads == 3
+        with pytest.raises(ValueError, match="max_seq_len"):
+            p.step(q, q, q)
+        assert c.lengths == (7,)
+        with torch.cuda.stream(torch.cuda.Stream()):
+            with pytest.raises(ValueError, match="cross-stream"):
+                p.attend(q)
+    with pytest.raises(ValueError, match="closed"):
+        p.step(q, q, q)
+    assert c.lengths == (7,)
+
+
+def test_workspace_alias_and_output_reuse(cuda_device):
+    c = _paged()(1, 8, 1, 8, page_size=3, chunk_size=4)
+    q = torch.ones((1, 1, 8), device="cuda", dtype=c.dtype)
+    with c.prepare_decode([0], 1, check_finite=False) as p:
+        with pytest.raises(ValueError, match="aliases"):
+            p.step(p.v, p.k, p.q)
+        a = p.step(q, q, q)
+        b = p.step(q, q, q)
+        assert a.output.data_ptr() == b.output.data_ptr()
+
+
+def test_capture_after_live_steps_and_capacity_boundary(cuda_device):
+    c = _paged()(1, 4, 1, 8, page_size=1, chunk_size=2)
+    q = torch.ones(1, 1, 8, device="cuda", dtype=c.dtype)
+    with c.prepare_decode([0], 1) as p:
+        for value in (1, 2, 3):
+            p.step(q, q, q * value)
+        before = c.materialize(0)
+        p.capture("step").capture("attend")
+        assert c.lengths == (3,)
+        after = c.materialize(0)
+        assert torch.equal(before[0], after[0]) and torch.equal(before[1], after[1])
+        check(c, p.step(q, q, q * 4, use_graph=True), q)
+        with pytest.raises(ValueError, match="max_seq_len"):
+            p.step(q, q, q, use_graph=True)
+        assert c.lengths == (4,)
+
+
+def test_graph_closes_large_chunk_at_max_head_dim(cuda_device):
+    c = _paged()(1, 1026, 1, 256, page_size=7, chunk_size=1024)
+    k, v = rand((1023, 1, 256), c.dtype, 801), rand((1023, 1, 256), c.dtype, 802)
+    c.append(k, v, sequence_ids=[0], cu_seqlens=[0, 1023])
+    q = rand((1, 4, 256), c.dtype, 803)
+    with c.prepare_decode([0], 4) as p:
+        p.capture("step")
+        check(c, p.step(q, k[:1], v[:1], use_graph=True), q)
+
+
+def test_bound_input_buffers_graph_without_staging(cuda_device):
+    c = _paged()(1, 8, 1, 1, page_size=4, chunk_size=2)
+    with c.prepare_decode([0], 1, check_finite=False) as p:
+        p.q.fill_(1)
+        p.k.fill_(1)
+        p.v.fill_(2)
+        p.capture("step")
+        for _ in range(3):
+            result = p.step(p.q, p.k, p.v, use_graph=True)
+            assert torch.equal(result.output, torch.full_like(result.output, 2))
+        assert p.delta_uploads == 1
+        with pytest.raises(ValueError, match="owns cache"):
+            c.prepare_decode([0], 1)
+
+
+def test_graph_replays_match_eager(cuda_device):
+    """Several replays with eager work and syncs in between; every replay must
+    equal the eager result bit-for-bit."""
+    dtype = torch.bfloat16
+    P = _paged()
+    eager = P(2, 200, 2, 64, page_size=5, chunk_size=8, dtype=dtype)
+    graphed = P(2, 200, 2, 64, page_size=5, chunk_size=8, dtype=dtype)
+    k, v = rand((90, 2, 64), dtype, 901), rand((90, 2, 64), dtype, 902)
+    for c in (eager, graphed):
+        c.append(k, v, sequence_ids=[0, 1], cu_seqlens=[0, 40, 90])
+    with eager.prepare_decode([0, 1], 12, topk=4) as pe, \
+            graphed.prepare_decode([0, 1], 12, topk=4) as pg:
+        pg.capture("step")
+        for step in range(12):
+            q = rand((2, 12, 64), dtype, 910 + step)
+            kn, vn = rand((2, 2, 64), dtype, 930 + step), rand((2, 2, 64), dtype, 950 + step)
+            a = pe.step(q, kn, vn)
+            _ = torch.randn(1000, device="cuda").sum().item()  # eager work between replays
+            b = pg.step(q, kn, vn, use_graph=True)
+            torch.cuda.synchronize()
+            assert torch.equal(a.output, b.output) and torch.equal(a.lse, b.lse)
+            assert torch.equal(a.selected_blocks, b.selected_blocks)
