@@ -93,6 +93,8 @@ int moba_hip_prefill_fwd(const void* q, const void* k, const void* v, int dtype,
  * filtered index or -1) tiles of 128 keys (64 when D > 128).  delta [T*Hq] and
  * part_dq [T*Hq*R, D] fp32 are workspaces.  dq [T,Hq,D], dk/dv [T,Hkv,D]
  * (dtype) are fully written (every key belongs to exactly one kv tile).
+ * parts selects the launches: 1 = Delta and dq (query-major kernels), 2 = dk/dv
+ * (key-major kernel, needs the Delta of a parts-1 call), 3 = both in order.
  * Deterministic: no atomics, fixed reduction order. */
 int moba_hip_prefill_bwd(const void* q, const void* k, const void* v, const void* out,
                          const void* dout, const float* lse, int dtype, int T, int Hq, int Hkv,
@@ -101,7 +103,7 @@ int moba_hip_prefill_bwd(const void* q, const void* k, const void* v, const void
                          int R, const int* filtered, int E, const int* tile_off,
                          const int* row_off, const int* counts, const int* rows,
                          int max_remote_tiles, float* delta, float* part_dq, void* dq, void* dk,
-                         void* dv, void* stream);
+                         void* dv, int parts, void* stream);
 
 /* ----------------------------------------------------------------- decode */
 

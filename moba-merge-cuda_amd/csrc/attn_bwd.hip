@@ -446,15 +446,17 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdArgs a) {
 }
 
 template <int DT, int DP>
-int launch_bwd(const BwdArgs& a, int n_self, int n_kv, int max_remote, hipStream_t st) {
+int launch_bwd(const BwdArgs& a, int n_self, int n_kv, int max_remote, int parts, hipStream_t st) {
   const int64_t rows = (int64_t)a.T * a.Hq;
-  hipLaunchKernelGGL(delta_kernel<DT>, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, st,
-                     a.out, a.dout, rows, a.D, a.delta);
-  if (max_remote > 0 && a.R > 0)
-    hipLaunchKernelGGL((dq_kernel<DT, DP, true, DP <= 128 ? 2 : 1>), dim3(max_remote), dim3(256), 0, st, a);
-  if (n_self > 0)
-    hipLaunchKernelGGL((dq_kernel<DT, DP, false, DP <= 128 ? 2 : 1>), dim3(n_self, a.Hq), dim3(256), 0, st, a);
-  if (n_kv > 0) {
+  if (parts & 1) {
+    hipLaunchKernelGGL(delta_kernel<DT>, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, st,
+                       a.out, a.dout, rows, a.D, a.delta);
+    if (max_remote > 0 && a.R > 0)
+      hipLaunchKernelGGL((dq_kernel<DT, DP, true, DP <= 128 ? 2 : 1>), dim3(max_remote), dim3(256), 0, st, a);
+    if (n_self > 0)
+      hipLaunchKernelGGL((dq_kernel<DT, DP, false, DP <= 128 ? 2 : 1>), dim3(n_self, a.Hq), dim3(256), 0, st, a);
+  }
+  if ((parts & 2) && n_kv > 0) {
     if constexpr (DP > 128)
       hipLaunchKernelGGL((dkdv_kernel<DT, DP, 2>), dim3(n_kv, a.Hkv), dim3(256), 0, st, a);
     else
@@ -464,11 +466,11 @@ int launch_bwd(const BwdArgs& a, int n_self, int n_kv, int max_remote, hipStream
 }
 
 template <int DT>
-int dispatch_bwd(const BwdArgs& a, int n_self, int n_kv, int max_remote, hipStream_t st) {
-  if (a.D <= 32) return launch_bwd<DT, 32>(a, n_self, n_kv, max_remote, st);
-  if (a.D <= 64) return launch_bwd<DT, 64>(a, n_self, n_kv, max_remote, st);
-  if (a.D <= 128) return launch_bwd<DT, 128>(a, n_self, n_kv, max_remote, st);
-  return launch_bwd<DT, 256>(a, n_self, n_kv, max_remote, st);
+int dispatch_bwd(const BwdArgs& a, int n_self, int n_kv, int max_remote, int parts, hipStream_t st) {
+  if (a.D <= 32) return launch_bwd<DT, 32>(a, n_self, n_kv, max_remote, parts, st);
+  if (a.D <= 64) return launch_bwd<DT, 64>(a, n_self, n_kv, max_remote, parts, st);
+  if (a.D <= 128) return launch_bwd<DT, 128>(a, n_self, n_kv, max_remote, parts, st);
+  return launch_bwd<DT, 256>(a, n_self, n_kv, max_remote, parts, st);
 }
 
 }  // namespace
@@ -481,11 +483,12 @@ extern "C" int moba_hip_prefill_bwd(const void* q, const void* k, const void* v,
                                     int E, const int* tile_off, const int* row_off,
                                     const int* counts, const int* rows, int max_remote_tiles,
                                     float* delta, float* part_dq, void* dq, void* dk, void* dv,
-                                    void* stream) {
+                                    int parts, void* stream) {
   if (dtype != 0 && dtype != 1) { moba_set_error("prefill_bwd: dtype must be 0 (bf16) or 1 (fp16)"); return MOBA_ERR_ARG; }
   if (D < 8 || D > 256 || D % 8) { moba_set_error("prefill_bwd: head_dim must be a multiple of 8 in [8,256]"); return MOBA_ERR_ARG; }
   if (Hq < 1 || Hkv < 1 || Hq % Hkv) { moba_set_error("prefill_bwd: Hq must be a positive multiple of Hkv"); return MOBA_ERR_ARG; }
   if (R < 0 || R > 8) { moba_set_error("prefill_bwd: remote count must be in [0,8]"); return MOBA_ERR_ARG; }
+  if (parts < 1 || parts > 3) { moba_set_error("prefill_bwd: parts must be 1 (dq), 2 (dk/dv) or 3 (both)"); return MOBA_ERR_ARG; }
   BwdArgs a;
   a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v;
   a.out = (const uint16_t*)out; a.dout = (const uint16_t*)dout; a.lse = lse;
@@ -498,6 +501,6 @@ extern "C" int moba_hip_prefill_bwd(const void* q, const void* k, const void* v,
   a.dq = (uint16_t*)dq; a.dk = (uint16_t*)dk; a.dv = (uint16_t*)dv;
   hipStream_t st = (hipStream_t)stream;
   const int mr = R > 0 ? max_remote_tiles : 0;
-  return dtype == 0 ? dispatch_bwd<0>(a, n_self_tiles, n_kv_tiles, mr, st)
-                    : dispatch_bwd<1>(a, n_self_tiles, n_kv_tiles, mr, st);
+  return dtype == 0 ? dispatch_bwd<0>(a, n_self_tiles, n_kv_tiles, mr, parts, st)
+                    : dispatch_bwd<1>(a, n_self_tiles, n_kv_tiles, mr, parts, st);
 }

@@ -56,6 +56,7 @@ __global__ void append_kernel(const uint16_t* __restrict__ k, const uint16_t* __
   const int n = (int)(idx / ((int64_t)D * Hkv));
   const int sid = seq[n], p = pos[n];
   const int page = table[(int64_t)sid * W + p / P];
+  if (page < 0) return;  // unmapped logical page: never write outside the pool
   const int64_t dst = (((int64_t)page * P + p % P) * Hkv + hk) * D + d;
   kc[dst] = k[idx];
   vc[dst] = v[idx];
@@ -74,6 +75,7 @@ __global__ void append_vec_kernel(const uint16_t* __restrict__ k, const uint16_t
   const int n = (int)(idx / ((int64_t)nd * Hkv));
   const int sid = seq[n], p = pos[n];
   const int page = table[(int64_t)sid * W + p / P];
+  if (page < 0) return;  // unmapped logical page: never write outside the pool
   const int64_t dst = (((int64_t)page * P + p % P) * Hkv + hk) * D + dc;
   const int64_t src = ((int64_t)n * Hkv + hk) * D + dc;
   st8(kc + dst, ld8(k + src));
@@ -104,7 +106,9 @@ __global__ void means_kernel(const uint16_t* __restrict__ kc, int Hkv, int D, in
   const int* trow = table + (int64_t)sid * W;
   float acc = 0.0f;
   for (int t = chunk * C; t < (chunk + 1) * C; ++t) {
-    const int64_t off = (((int64_t)trow[t / P] * P + t % P) * Hkv + hk) * D + d;
+    const int page = trow[t / P];
+    if (page < 0) continue;  // unmapped page (caller bug): read nothing
+    const int64_t off = (((int64_t)page * P + t % P) * Hkv + hk) * D + d;
     acc = acc + to_f32<DT>(kc[off]);
   }
   means[(((int64_t)sid * max_chunks + chunk) * Hkv + hk) * D + d] = from_f32<DT>(acc / (float)C);
@@ -245,8 +249,9 @@ __global__ __launch_bounds__(64) void attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       const int tok = tt + half * 16 + c16;
-      const bool tok_ok = tok < t1;
-      const int64_t base = tok_ok ? (((int64_t)trow[tok / a.P] * a.P + tok % a.P) * a.Hkv + kh) * D : 0;
+      const int page = tok < t1 ? trow[tok / a.P] : -1;
+      const bool tok_ok = page >= 0;  // unmapped pages read as zero, never out of the pool
+      const int64_t base = tok_ok ? (((int64_t)page * a.P + tok % a.P) * a.Hkv + kh) * D : 0;
       sc[half] = (f32x4v){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {
@@ -266,8 +271,9 @@ __global__ __launch_bounds__(64) void attn_kernel(AttnArgs a) {
       const int r = id / (DP / 8), dc = (id % (DP / 8)) * 8;
       const int tok = tt + r;
       u16x8_t vv = zero8();
-      if (tok < t1) {
-        const int64_t base = (((int64_t)trow[tok / a.P] * a.P + tok % a.P) * a.Hkv + kh) * D;
+      const int page = tok < t1 ? trow[tok / a.P] : -1;
+      if (page >= 0) {
+        const int64_t base = (((int64_t)page * a.P + tok % a.P) * a.Hkv + kh) * D;
         if constexpr (VEC) {
           if (dc < D) vv = ld8(a.vc + base + dc);
         } else {

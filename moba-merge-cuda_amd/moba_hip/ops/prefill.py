@@ -168,6 +168,11 @@ def forward(plan: PrefillPlan, q, k, v, rt: RouteResult | None):
     return out, lse
 
 
+# Optional (start, stop) torch.cuda.Event pair recorded around the key-major
+# dK/dV launch of every backward (used by bench.py to time that kernel live).
+DKDV_EVENTS = None
+
+
 def backward(plan: PrefillPlan, q, k, v, out, lse, dout, rt: RouteResult | None):
     """Gradients (dq, dk, dv) of ``forward`` for the upstream gradient ``dout``."""
     T, hq, d = q.shape
@@ -176,13 +181,21 @@ def backward(plan: PrefillPlan, q, k, v, out, lse, dout, rt: RouteResult | None)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     delta = torch.empty(T * hq, dtype=torch.float32, device=dev)
     part_dq = torch.empty((T * hq * R, d), dtype=torch.float32, device=dev) if R else None
-    _lib.call("moba_hip_prefill_bwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-              dout.data_ptr(), lse.data_ptr(), DTYPE_CODE[q.dtype], T, hq, plan.hkv, d,
-              d ** -0.5, plan.ptr("att_chunk"), plan.ptr("self_tiles"), plan.n_self_tiles,
-              plan.ptr("kv_tiles"), plan.n_kv_tiles,
-              _lib.ptr(rt.sel) if R else None, R, plan.ptr("filtered"), plan.num_experts,
-              _lib.ptr(rt.tile_off) if R else None, _lib.ptr(rt.row_off) if R else None,
-              _lib.ptr(rt.counts) if R else None, _lib.ptr(rt.rows) if R else None,
-              plan.max_remote_tiles if R else 0, delta.data_ptr(), _lib.ptr(part_dq),
-              dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), _lib.stream_of(dev))
+    args = [q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+            dout.data_ptr(), lse.data_ptr(), DTYPE_CODE[q.dtype], T, hq, plan.hkv, d,
+            d ** -0.5, plan.ptr("att_chunk"), plan.ptr("self_tiles"), plan.n_self_tiles,
+            plan.ptr("kv_tiles"), plan.n_kv_tiles,
+            _lib.ptr(rt.sel) if R else None, R, plan.ptr("filtered"), plan.num_experts,
+            _lib.ptr(rt.tile_off) if R else None, _lib.ptr(rt.row_off) if R else None,
+            _lib.ptr(rt.counts) if R else None, _lib.ptr(rt.rows) if R else None,
+            plan.max_remote_tiles if R else 0, delta.data_ptr(), _lib.ptr(part_dq),
+            dq.data_ptr(), dk.data_ptr(), dv.data_ptr()]
+    st = _lib.stream_of(dev)
+    _lib.call("moba_hip_prefill_bwd", *args, 1, st)
+    events = DKDV_EVENTS
+    if events is not None:
+        events[0].record()
+    _lib.call("moba_hip_prefill_bwd", *args, 2, st)
+    if events is not None:
+        events[1].record()
     return dq, dk, dv

@@ -1,0 +1,114 @@
+"""CPU contract tests: validation envelope, registry, cache constructor
+errors before any GPU work, and the C-ABI library surface (loads and exports
+every symbol include/moba_hip.h declares; argument errors return without
+touching a device)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from moba_hip import api
+from moba_hip.baseline_adapter import validate_config, validate_shapes
+from moba_hip.kv_cache import PagedKVCache, _mode
+from moba_hip.ops import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+@pytest.mark.parametrize("hq,hkv", [(1, 1), (28, 4), (32, 8), (16, 2), (8, 1), (14, 2)])
+def test_grouped_shapes(hq, hkv):
+    assert validate_shapes((11, hq, 128), (11, hkv, 128), (11, hkv, 128), True) == hq // hkv
+
+
+@pytest.mark.parametrize("dim", range(8, 257, 8))
+def test_head_dimensions(dim):
+    assert validate_shapes((3, 2, dim), (3, 2, dim), (3, 2, dim)) == 1
+
+
+@pytest.mark.parametrize("qs,ks,vs", [
+    ((0, 2, 64), (0, 2, 64), (0, 2, 64)), ((3, 3, 64), (3, 2, 64), (3, 2, 64)),
+    ((3, 2, 7), (3, 2, 7), (3, 2, 7)), ((3, 2, 264), (3, 2, 264), (3, 2, 264)),
+    ((3, 2, 64), (4, 2, 64), (4, 2, 64)), ((3, 2, 64), (3, 1, 64), (3, 2, 64)),
+])
+def test_invalid_shapes(qs, ks, vs):
+    with pytest.raises(ValueError):
+        validate_shapes(qs, ks, vs, True)
+
+
+def test_mha_only_entry_rejects_gqa():
+    with pytest.raises(ValueError, match="MHA only"):
+        validate_shapes((3, 4, 64), (3, 2, 64), (3, 2, 64), False)
+
+
+@pytest.mark.parametrize("override", [
+    {"chunk_size": 0}, {"chunk_size": True}, {"topk": 0}, {"topk": 10},
+    {"topk": 2.5}, {"causal": False}, {"dropout": 0.1},
+])
+def test_invalid_configs(override):
+    with pytest.raises(ValueError):
+        validate_config({"chunk_size": 32, "topk": 4, **override})
+
+
+def test_registry_contract():
+    assert {"opt_hip", "opt_merge_hip"} <= set(api.available_impls())
+    with pytest.raises(KeyError, match="already registered"):
+        api.register("opt_hip", lambda *a: None)
+    with pytest.raises(KeyError, match="unknown impl"):
+        api.run_impl("nope", None, None, None, None, None, None)
+
+
+def test_prefill_rejects_cpu_tensors():
+    q = torch.randn(8, 2, 64).bfloat16()
+    cu = torch.tensor([0, 8], dtype=torch.int32)
+    with pytest.raises(ValueError, match="CUDA"):
+        api.run_impl("opt_hip", q, q, q, cu, 8, {"chunk_size": 4, "topk": 3})
+
+
+@pytest.mark.parametrize("kwargs", [
+    {"head_dim": 0}, {"head_dim": 264}, {"num_kv_heads": 0}, {"page_size": 0},
+    {"num_pages": 0}, {"chunk_size": 1025}, {"dtype": torch.float32}, {"device": "cpu"},
+])
+def test_cache_contract_before_gpu_initialization(kwargs):
+    cfg = dict(batch_size=1, max_seq_len=16, num_kv_heads=2, head_dim=64)
+    cfg.update(kwargs)
+    with pytest.raises(ValueError):
+        PagedKVCache(**cfg)
+
+
+@pytest.mark.parametrize("mode,topk", [("other", 4), ("dense", 0), ("moba", 10), ("moba", True)])
+def test_decode_mode_contract(mode, topk):
+    with pytest.raises(ValueError):
+        _mode(mode, topk)
+
+
+def _declared_symbols():
+    text = (ROOT / "include" / "moba_hip.h").read_text()
+    return sorted(set(re.findall(r"\b(moba_hip_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    names = _declared_symbols()
+    assert len(names) >= 13
+    for name in names:
+        assert hasattr(lib, name), f"{name} missing from libmoba_hip.so"
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signatures out of sync with the header"
+    assert _lib.load().moba_hip_version() == 1
+
+
+def test_argument_errors_are_reported_without_a_device():
+    with pytest.raises(_lib.MobaHipError, match="dtype"):
+        _lib.call("moba_hip_prefill_fwd", None, None, None, 7, 1, 1, 1, 64, 1.0, None, None, 0,
+                  None, 0, None, 0, None, None, None, None, 0, None, None, None, None, None)
+    with pytest.raises(_lib.MobaHipError, match="head_dim"):
+        _lib.call("moba_hip_prefill_bwd", None, None, None, None, None, None, 0, 1, 1, 1, 12,
+                  1.0, None, None, 0, None, 0, None, 0, None, 0, None, None, None, None, 0,
+                  None, None, None, None, None, 3, None)
+    with pytest.raises(_lib.MobaHipError, match="remote count"):
+        _lib.call("moba_hip_route_prefill", None, 0, 1, 1, 1, 8, None, None, 1, None, None, 9, 1,
+                  None, None, None)
+    with pytest.raises(_lib.MobaHipError, match="head_dim"):
+        _lib.call("moba_hip_paged_attention", None, 0, 1, 1, 1, 300, None, None, 1, None, 1,
+                  None, None, None, None, 1, 0, 4, 1, None, None, None, None, None)

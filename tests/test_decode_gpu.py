@@ -266,3 +266,21 @@ def test_append_rejects_aliases_before_mutation(cuda_device, combined):
     assert cache.lengths == (0,)
     cache.append(external, external, sequence_ids=[0])
     assert cache.lengths == (1,)
+
+
+def test_unmapped_page_is_never_written(cuda_device):
+    """Regression: a token whose logical page has no physical page (table
+    entry -1) must not be written anywhere in the pool (the append kernel once
+    computed a negative address for it)."""
+    from moba_hip.ops import decode as kernels
+    Paged, _ = _caches()
+    cache = Paged(2, 16, 1, 8, page_size=4, chunk_size=4)
+    cache.k_cache.zero_()
+    cache.v_cache.zero_()
+    table = torch.full((2, 4), -1, dtype=torch.int32, device="cuda")
+    k = torch.ones((1, 1, 8), device="cuda", dtype=cache.dtype)
+    ids = torch.tensor([1], dtype=torch.int32, device="cuda")
+    pos = torch.tensor([5], dtype=torch.int32, device="cuda")
+    kernels.append_tokens(k, k, cache.k_cache, cache.v_cache, table, ids, pos)
+    torch.cuda.synchronize()
+    assert int(cache.k_cache.count_nonzero()) == 0 and int(cache.v_cache.count_nonzero()) == 0
