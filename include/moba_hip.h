@@ -40,7 +40,9 @@ int moba_hip_version(void);
  * src/moba_opt/grouped_attention.py:48-52 (diagnostic.py:391-399).
  * k [T,Hkv,D]; chunk_start[F] first token of each candidate chunk;
  * precision 0 = "upstream" (mean rounded to dtype), 1 = "fp32".
- * means [F,Hkv,D] fp32.  Canonical order: sequential fp32 sum, / chunk. */
+ * means [F,Hkv,D] fp32.  Canonical order: lane j of a wave sums tokens j,
+ * j+64, ...; the 64 partials are added by the fixed tree part[j] += part[j+off],
+ * off = 32..1; then / chunk (the CPU oracle implements the same order). */
 int moba_hip_chunk_means(const void* k, int dtype, int T, int Hkv, int D,
                          const int* chunk_start, int F, int chunk, int precision,
                          float* means, void* stream);
@@ -119,8 +121,9 @@ int moba_hip_paged_append(const void* k, const void* v, int dtype, int N, int Hk
                           int table_width, const int* token_seq, const int* token_pos,
                           void* stream);
 
-/* Key means of closed chunks into means [B, max_chunks, Hkv, D] (cache dtype),
- * fp32 sequential sum / chunk.  mode 0: item i = (item_seq[i], chunk
+/* Key means of closed chunks into means [B, max_chunks, Hkv, D] (cache dtype):
+ * canonical fp32 sum (64 strided partial sums, then a fixed pairwise tree),
+ * / chunk.  mode 0: item i = (item_seq[i], chunk
  * item_chunk_or_pos[i]); mode 1: item i = query row at position p, closing
  * chunk p / chunk only when (p + 1) % chunk == 0.
  * Replaces _closed_means_kernel (paged_decode.py:26-44) and _step_means
@@ -133,7 +136,8 @@ int moba_hip_block_means(const void* k_cache, int dtype, int Hkv, int D, int pag
 /* Route of decode queries q [Nq,Hq,D]: fp32 fma-chain scores against the means
  * of the closed chunks c with (c+1)*chunk <= pos, stable top-R (descending,
  * ties -> lowest chunk).  selected [Nq,Hq,1+R]: slot 0 = pos / chunk, then the
- * chosen chunks, -1 padded.  scores (nullable) [Nq,Hq,width].
+ * chosen chunks, -1 padded.  scores [Nq,Hq,width] (required when R > 0;
+ * -inf for illegal chunks).  Canonical fp32 means: see moba_hip_block_means.
  * Replaces _route_kernel + torch.topk / _stable_topk + _selected
  * (paged_decode.py:47-64, src/moba_opt/kv_cache.py:208-223,
  * prepared_decode.py:44-88). */

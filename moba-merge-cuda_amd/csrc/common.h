@@ -122,6 +122,16 @@ template <int DT> MOBA_DEV u16x8_t pack8(const float* v) {
   return r;
 }
 
+// Canonical fp32 reduction shared with the CPU oracle: lane j of a wave holds
+// the sequential sum of elements j, j+64, j+128, ...; the partials are then
+// added by the fixed tree part[j] += part[j+off], off = 32..1.  Lane 0 returns
+// the result (other lanes return partial values).
+MOBA_DEV float canon_tree(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = v + __shfl_down(v, off, 64);
+  return v;
+}
+
 MOBA_DEV float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));

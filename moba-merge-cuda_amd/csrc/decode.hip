@@ -83,20 +83,23 @@ __global__ void append_vec_kernel(const uint16_t* __restrict__ k, const uint16_t
 }
 
 // ------------------------------------------------------------------- means
+// One wave per (item, kv head, 8 consecutive d); lane j sums tokens j, j+64,
+// ... of the chunk through the page table, then the canonical tree.
 // mode 0: item i closes chunk chunk_or_pos[i] of sequence seq[i].
 // mode 1: item i is a query row at position chunk_or_pos[i]; it closes chunk
 //         pos / C only when (pos + 1) % C == 0 (prepared decode step).
-template <int DT>
-__global__ void means_kernel(const uint16_t* __restrict__ kc, int Hkv, int D, int P,
-                             const int* __restrict__ table, int W, const int* __restrict__ seq,
-                             const int* __restrict__ chunk_or_pos, int n_items, int mode, int C,
-                             uint16_t* __restrict__ means, int max_chunks) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t total = (int64_t)n_items * Hkv * D;
-  if (idx >= total) return;
-  const int d = (int)(idx % D);
-  const int hk = (int)((idx / D) % Hkv);
-  const int i = (int)(idx / ((int64_t)D * Hkv));
+template <int DT, bool VEC>
+__global__ __launch_bounds__(64) void means_kernel(const uint16_t* __restrict__ kc, int Hkv,
+                                                   int D, int P, const int* __restrict__ table,
+                                                   int W, const int* __restrict__ seq,
+                                                   const int* __restrict__ chunk_or_pos, int mode,
+                                                   int C, uint16_t* __restrict__ means,
+                                                   int max_chunks) {
+  const int nd8 = (D + 7) / 8;
+  const int db = blockIdx.x % nd8;
+  const int kh = (blockIdx.x / nd8) % Hkv;
+  const int i = blockIdx.x / (nd8 * Hkv);
+  const int lane = threadIdx.x;
   const int sid = seq[i];
   int chunk = chunk_or_pos[i];
   if (mode == 1) {
@@ -104,59 +107,89 @@ __global__ void means_kernel(const uint16_t* __restrict__ kc, int Hkv, int D, in
     chunk = chunk / C;
   }
   const int* trow = table + (int64_t)sid * W;
-  float acc = 0.0f;
-  for (int t = chunk * C; t < (chunk + 1) * C; ++t) {
+  const int d0 = db * 8;
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+  for (int t = chunk * C + lane; t < (chunk + 1) * C; t += 64) {
     const int page = trow[t / P];
     if (page < 0) continue;  // unmapped page (caller bug): read nothing
-    const int64_t off = (((int64_t)page * P + t % P) * Hkv + hk) * D + d;
-    acc = acc + to_f32<DT>(kc[off]);
+    const int64_t off = (((int64_t)page * P + t % P) * Hkv + kh) * D + d0;
+    if constexpr (VEC) {
+      const u16x8_t x = ld8(kc + off);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = acc[e] + to_f32<DT>(x[e]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (d0 + e < D) acc[e] = acc[e] + to_f32<DT>(kc[off + e]);
+    }
   }
-  means[(((int64_t)sid * max_chunks + chunk) * Hkv + hk) * D + d] = from_f32<DT>(acc / (float)C);
+  uint16_t res[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) res[e] = from_f32<DT>(canon_tree(acc[e]) / (float)C);
+  if (lane == 0) {
+    uint16_t* dst = means + (((int64_t)sid * max_chunks + chunk) * Hkv + kh) * D + d0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (d0 + e < D) dst[e] = res[e];
+  }
 }
 
 // ------------------------------------------------------------------- route
+// One wave per (query row, q head).  Lane j scores chunks j, j+64, ... (fp32
+// fma chain over d, the canonical gate order) against the cache-dtype means;
+// the stable top-R is R rounds of a wave argmax: each round takes the best
+// candidate strictly after the previous pick in (score desc, chunk asc) order.
 template <int DT>
-__global__ void route_kernel(const uint16_t* __restrict__ q, int Nq, int Hq, int Hkv, int D,
-                             const uint16_t* __restrict__ means, int max_chunks,
-                             const int* __restrict__ seq, const int* __restrict__ pos, int C,
-                             int width, int R, float* __restrict__ scores,
-                             int* __restrict__ selected) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (int64_t)Nq * Hq) return;
-  const int row = (int)(idx / Hq), h = (int)(idx % Hq);
+__global__ __launch_bounds__(64) void route_kernel(const uint16_t* __restrict__ q, int Hq, int Hkv,
+                                                   int D, const uint16_t* __restrict__ means,
+                                                   int max_chunks, const int* __restrict__ seq,
+                                                   const int* __restrict__ pos, int C, int width,
+                                                   int R, float* __restrict__ scores,
+                                                   int* __restrict__ selected) {
+  __shared__ float qs[256];
+  const int idx = blockIdx.x;  // row * Hq + h
+  const int row = idx / Hq, h = idx % Hq;
   const int kh = h / (Hq / Hkv);
+  const int lane = threadIdx.x;
   const int sid = seq[row], p = pos[row];
+  for (int d = lane; d < D; d += 64) qs[d] = to_f32<DT>(q[(int64_t)idx * D + d]);
+  __syncthreads();
   const int legal = min(p / C, width);  // chunks c with (c+1)*C <= p
-  const uint16_t* qr = q + idx * D;
-  float val[kMaxRemote];
-  int ix[kMaxRemote];
-  int cnt = 0;
-#pragma unroll
-  for (int j = 0; j < kMaxRemote; ++j) { val[j] = -INFINITY; ix[j] = -1; }
-  for (int c = 0; c < legal; ++c) {
-    const uint16_t* mr = means + (((int64_t)sid * max_chunks + c) * Hkv + kh) * D;
-    float acc = 0.0f;
-    for (int d = 0; d < D; ++d) acc = fmaf(to_f32<DT>(mr[d]), to_f32<DT>(qr[d]), acc);
-    if (scores) scores[idx * width + c] = acc;
-    if (R == 0 || (cnt == R && !(acc > val[R - 1]))) continue;
-    int p2 = 0;
-#pragma unroll
-    for (int j = 0; j < kMaxRemote; ++j) p2 += (j < cnt && val[j] >= acc);
-#pragma unroll
-    for (int j = kMaxRemote - 1; j >= 1; --j)
-      if (j > p2 && j < R) { val[j] = val[j - 1]; ix[j] = ix[j - 1]; }
-#pragma unroll
-    for (int j = 0; j < kMaxRemote; ++j)
-      if (j == p2) { val[j] = acc; ix[j] = c; }
-    if (cnt < R) cnt++;
+  float* srow = scores + (int64_t)idx * width;
+  for (int c = lane; c < width; c += 64) {
+    float acc = -INFINITY;
+    if (c < legal) {
+      const uint16_t* mr = means + (((int64_t)sid * max_chunks + c) * Hkv + kh) * D;
+      acc = 0.0f;
+      for (int d = 0; d < D; ++d) acc = fmaf(to_f32<DT>(mr[d]), qs[d], acc);
+    }
+    srow[c] = acc;
   }
-  if (scores)
-    for (int c = legal; c < width; ++c) scores[idx * width + c] = -INFINITY;
-  int* out = selected + idx * (R + 1);
-  out[0] = p / C;
+  __syncthreads();  // scores of this row are re-read by other lanes below
+  int* out = selected + (int64_t)idx * (R + 1);
+  if (lane == 0) out[0] = p / C;
+  float last_v = INFINITY;
+  int last_c = -1;
+  for (int r = 0; r < R; ++r) {
+    float bv = -INFINITY;
+    int bc = 0x7fffffff;
+    for (int c = lane; c < legal; c += 64) {
+      const float v = srow[c];
+      const bool after = v < last_v || (v == last_v && c > last_c);
+      if (after && (v > bv || (v == bv && c < bc))) { bv = v; bc = c; }
+    }
 #pragma unroll
-  for (int j = 0; j < kMaxRemote; ++j)
-    if (j < R) out[1 + j] = j < cnt ? ix[j] : -1;
+    for (int off = 32; off > 0; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, 64);
+      const int oc = __shfl_xor(bc, off, 64);
+      if (ov > bv || (ov == bv && oc < bc)) { bv = ov; bc = oc; }
+    }
+    const bool found = bv > -INFINITY;
+    if (lane == 0) out[1 + r] = found ? bc : -1;
+    if (found) { last_v = bv; last_c = bc; } else { last_v = -INFINITY; last_c = 0x7fffffff; }
+  }
 }
 
 // --------------------------------------------------------------- attention
@@ -461,17 +494,15 @@ extern "C" int moba_hip_block_means(const void* k_cache, int dtype, int Hkv, int
                                     void* means, int max_chunks, void* stream) {
   if (n_items <= 0) return MOBA_OK;
   if (dtype != 0 && dtype != 1) { moba_set_error("block_means: dtype must be 0 or 1"); return MOBA_ERR_ARG; }
-  const int64_t n = (int64_t)n_items * Hkv * D;
-  dim3 grid((unsigned)((n + 255) / 256)), block(256);
+  dim3 grid((unsigned)((int64_t)n_items * Hkv * ((D + 7) / 8))), block(64);
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == 0)
-    hipLaunchKernelGGL(means_kernel<0>, grid, block, 0, st, (const uint16_t*)k_cache, Hkv, D,
-                       page_size, table, table_width, item_seq, item_chunk_or_pos, n_items, mode,
-                       chunk, (uint16_t*)means, max_chunks);
-  else
-    hipLaunchKernelGGL(means_kernel<1>, grid, block, 0, st, (const uint16_t*)k_cache, Hkv, D,
-                       page_size, table, table_width, item_seq, item_chunk_or_pos, n_items, mode,
-                       chunk, (uint16_t*)means, max_chunks);
+#define MOBA_MEANS(DT_, VEC_)                                                                   \
+  hipLaunchKernelGGL((means_kernel<DT_, VEC_>), grid, block, 0, st, (const uint16_t*)k_cache,   \
+                     Hkv, D, page_size, table, table_width, item_seq, item_chunk_or_pos, mode,  \
+                     chunk, (uint16_t*)means, max_chunks)
+  if (D % 8 == 0) { if (dtype == 0) MOBA_MEANS(0, true); else MOBA_MEANS(1, true); }
+  else { if (dtype == 0) MOBA_MEANS(0, false); else MOBA_MEANS(1, false); }
+#undef MOBA_MEANS
   return moba_launch_status("block_means");
 }
 
@@ -481,18 +512,19 @@ extern "C" int moba_hip_decode_route(const void* q, int dtype, int Nq, int Hq, i
                                      int* selected, void* stream) {
   if (R < 0 || R > kMaxRemote) { moba_set_error("decode_route: remote count must be in [0,8]"); return MOBA_ERR_ARG; }
   if (Hq % Hkv) { moba_set_error("decode_route: Hq must be a multiple of Hkv"); return MOBA_ERR_ARG; }
+  if (D < 1 || D > 256) { moba_set_error("decode_route: head_dim must be in [1,256]"); return MOBA_ERR_ARG; }
+  if (R > 0 && (scores == nullptr || width < 1)) { moba_set_error("decode_route: scores workspace [Nq,Hq,width] required"); return MOBA_ERR_ARG; }
   const int64_t n = (int64_t)Nq * Hq;
   if (n == 0) return MOBA_OK;
-  dim3 grid((unsigned)((n + 127) / 128)), block(128);
   hipStream_t st = (hipStream_t)stream;
   if (dtype == 0)
-    hipLaunchKernelGGL(route_kernel<0>, grid, block, 0, st, (const uint16_t*)q, Nq, Hq, Hkv, D,
-                       (const uint16_t*)means, max_chunks, q_seq, q_pos, chunk, width, R, scores,
-                       selected);
+    hipLaunchKernelGGL(route_kernel<0>, dim3((unsigned)n), dim3(64), 0, st, (const uint16_t*)q, Hq,
+                       Hkv, D, (const uint16_t*)means, max_chunks, q_seq, q_pos, chunk, width, R,
+                       scores, selected);
   else
-    hipLaunchKernelGGL(route_kernel<1>, grid, block, 0, st, (const uint16_t*)q, Nq, Hq, Hkv, D,
-                       (const uint16_t*)means, max_chunks, q_seq, q_pos, chunk, width, R, scores,
-                       selected);
+    hipLaunchKernelGGL(route_kernel<1>, dim3((unsigned)n), dim3(64), 0, st, (const uint16_t*)q, Hq,
+                       Hkv, D, (const uint16_t*)means, max_chunks, q_seq, q_pos, chunk, width, R,
+                       scores, selected);
   return moba_launch_status("decode_route");
 }
 

@@ -5,8 +5,9 @@
 // (stack/index_select, mean, einsum, mask, topk/argmax loop, nonzero packing).
 // The arithmetic order is the canonical one of the CPU oracle, so the selected
 // block sets are bit-identical to it:
-//   mean  = sequential fp32 sum over the chunk's tokens, / C  (optionally
-//           rounded to the input dtype: route_precision "upstream")
+//   mean  = canonical fp32 sum over the chunk's tokens (64 strided partial
+//           sums + fixed pairwise tree), / C  (optionally rounded to the
+//           input dtype: route_precision "upstream")
 //   gate  = fma chain over d = 0..D-1 in fp32
 //   top-k = descending gate, exact ties -> lowest chunk, -inf never chosen.
 #include "common.h"
@@ -18,33 +19,40 @@ namespace {
 
 constexpr int kMaxRemote = 8;
 
-// One thread per (filtered chunk, kv head, d): coalesced over d.
+// One wave per (filtered chunk, kv head, 8 consecutive d): lane j sums the
+// tokens j, j+64, ... (16-byte loads), then the canonical tree.
 template <int DT>
-__global__ void chunk_means_kernel(const uint16_t* __restrict__ k, int Hkv, int D,
-                                   const int* __restrict__ chunk_start, int F, int C,
-                                   int precision, float* __restrict__ means) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t total = (int64_t)F * Hkv * D;
-  if (idx >= total) return;
-  const int d = (int)(idx % D);
-  const int h = (int)((idx / D) % Hkv);
-  const int f = (int)(idx / ((int64_t)D * Hkv));
-  const uint16_t* p = k + ((int64_t)chunk_start[f] * Hkv + h) * D + d;
+__global__ __launch_bounds__(64) void chunk_means_kernel(const uint16_t* __restrict__ k, int Hkv,
+                                                         int D, const int* __restrict__ chunk_start,
+                                                         int C, int precision,
+                                                         float* __restrict__ means) {
+  const int nd8 = D / 8;
+  const int db = blockIdx.x % nd8;
+  const int kh = (blockIdx.x / nd8) % Hkv;
+  const int f = blockIdx.x / (nd8 * Hkv);
+  const int lane = threadIdx.x;
+  const uint16_t* p = k + ((int64_t)chunk_start[f] * Hkv + kh) * D + db * 8;
   const int64_t stride = (int64_t)Hkv * D;
-  float acc = 0.0f;
-  int t = 0;
-  // Sequential order is the contract; the unroll only batches the loads.
-  for (; t + 4 <= C; t += 4) {
-    float a0 = to_f32<DT>(p[(t + 0) * stride]);
-    float a1 = to_f32<DT>(p[(t + 1) * stride]);
-    float a2 = to_f32<DT>(p[(t + 2) * stride]);
-    float a3 = to_f32<DT>(p[(t + 3) * stride]);
-    acc = acc + a0; acc = acc + a1; acc = acc + a2; acc = acc + a3;
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+  for (int t = lane; t < C; t += 64) {
+    const u16x8_t x = ld8(p + t * stride);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = acc[e] + to_f32<DT>(x[e]);
   }
-  for (; t < C; ++t) acc = acc + to_f32<DT>(p[t * stride]);
-  float m = acc / (float)C;
-  if (precision == 0) m = to_f32<DT>(from_f32<DT>(m));
-  means[idx] = m;
+  float out[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float m = canon_tree(acc[e]) / (float)C;
+    if (precision == 0) m = to_f32<DT>(from_f32<DT>(m));
+    out[e] = m;
+  }
+  if (lane == 0) {
+    float* dst = means + ((int64_t)f * Hkv + kh) * D + db * 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dst[e] = out[e];
+  }
 }
 
 // One thread per (token, q head); heads fastest so a wave reads adjacent q rows.
@@ -242,16 +250,15 @@ extern "C" int moba_hip_chunk_means(const void* k, int dtype, int T, int Hkv, in
   (void)T;
   if (F <= 0) return MOBA_OK;
   if (dtype != 0 && dtype != 1) { moba_set_error("chunk_means: dtype must be 0 (bf16) or 1 (fp16)"); return MOBA_ERR_ARG; }
-  if (D < 1 || Hkv < 1 || chunk < 1) { moba_set_error("chunk_means: bad shape"); return MOBA_ERR_ARG; }
-  const int64_t total = (int64_t)F * Hkv * D;
-  dim3 grid((unsigned)((total + 255) / 256)), block(256);
+  if (D < 8 || D % 8 || Hkv < 1 || chunk < 1) { moba_set_error("chunk_means: bad shape"); return MOBA_ERR_ARG; }
+  dim3 grid((unsigned)((int64_t)F * Hkv * (D / 8))), block(64);
   hipStream_t st = (hipStream_t)stream;
   if (dtype == 0)
     hipLaunchKernelGGL(chunk_means_kernel<0>, grid, block, 0, st, (const uint16_t*)k, Hkv, D,
-                       chunk_start, F, chunk, precision, means);
+                       chunk_start, chunk, precision, means);
   else
     hipLaunchKernelGGL(chunk_means_kernel<1>, grid, block, 0, st, (const uint16_t*)k, Hkv, D,
-                       chunk_start, F, chunk, precision, means);
+                       chunk_start, chunk, precision, means);
   return moba_launch_status("chunk_means");
 }
 

@@ -232,8 +232,10 @@ class PagedKVCache:
         if remote and width * hq * nq >= 2 ** 31:
             raise ValueError("route score grid exceeds int32 capacity")
         selected = torch.empty((nq, hq, 1 + remote), dtype=torch.int32, device=self.device)
+        scores = (torch.empty((nq, hq, width), dtype=torch.float32, device=self.device)
+                  if remote else None)
         kernels.route(q, self._means, ids, positions, self.chunk_size, width if remote else 0,
-                      remote, None, selected)
+                      remote, scores, selected)
         return selected
 
     @torch.no_grad()

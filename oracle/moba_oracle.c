@@ -9,7 +9,10 @@
  *     decode block means and decode route scores).  The summation order is
  *     DEFINED here and implemented identically by the HIP kernels, so block
  *     selection can be compared bit-for-bit:
- *        mean[d]   = (((k[t0][d] + k[t0+1][d]) + k[t0+2][d]) + ...) / C     (fp32)
+ *        mean[d]   = tree64(part) / C  (fp32), part[j] = sequential sum of the
+ *                    tokens t = j, j+64, j+128, ... of the chunk (0.0f start),
+ *                    tree64: for off = 32,16,8,4,2,1: part[j] += part[j+off]
+ *                    (j < off); the result is part[0]
  *        gate      = fma(mean[D-1], q[D-1], ... fma(mean[1], q[1], fma(mean[0], q[0], 0)))
  *        top-k     = descending score, exact ties -> lowest chunk index,
  *                    -inf (illegal) never selected.
@@ -98,7 +101,22 @@ void oracle_set_threads(int n) {
 
 /* ----------------------------------------------------- canonical routing */
 
-/* Sequential fp32 sum over C consecutive tokens, then / C.
+/* Canonical fp32 sum of n values x(t), t = 0..n-1: 64 strided partial sums
+ * (lane j of a wave owns t = j, j+64, ...), then a fixed pairwise tree. */
+#define CANON_SUM(n, x_of_t, result)                                          \
+  do {                                                                        \
+    float part_[64];                                                          \
+    for (int j_ = 0; j_ < 64; ++j_) {                                         \
+      float a_ = 0.0f;                                                        \
+      for (int t = j_; t < (n); t += 64) a_ = a_ + (x_of_t);                  \
+      part_[j_] = a_;                                                         \
+    }                                                                         \
+    for (int off_ = 32; off_ > 0; off_ >>= 1)                                 \
+      for (int j_ = 0; j_ < off_; ++j_) part_[j_] = part_[j_] + part_[j_ + off_]; \
+    (result) = part_[0];                                                      \
+  } while (0)
+
+/* Chunk means of the F routing candidates, canonical sum, then / C.
  * precision 0 ("upstream"): the mean is rounded to the input dtype and widened
  * back (torch's keys.mean(1).float(), grouped_attention.py:52);
  * precision 1 ("fp32"): kept in fp32 (keys.float().mean(1)). */
@@ -109,9 +127,8 @@ void oracle_chunk_means(const uint16_t* k, int dtype, int T, int Hkv, int D,
   for (int f = 0; f < F; ++f)
     for (int h = 0; h < Hkv; ++h)
       for (int d = 0; d < D; ++d) {
-        float acc = 0.0f;
-        for (int t = 0; t < C; ++t)
-          acc = acc + to_f32(k[((size_t)(chunk_start[f] + t) * Hkv + h) * D + d], dtype);
+        float acc;
+        CANON_SUM(C, to_f32(k[((size_t)(chunk_start[f] + t) * Hkv + h) * D + d], dtype), acc);
         float m = acc / (float)C;
         if (precision == 0) m = oracle_round_to_dtype(m, dtype);
         means[((size_t)f * Hkv + h) * D + d] = m;
@@ -331,15 +348,15 @@ void oracle_merge(const double* self_out, const double* self_lse, int P, int D,
 
 /* Closed-chunk means of one sequence's logical keys k[L,Hkv,D] (bits), stored
  * in the cache dtype (paged_decode.py:26-44 stores tl.sum/C into a cache-dtype
- * tensor).  Canonical order as above.  out[nclosed,Hkv,D] bits. */
+ * tensor).  Canonical sum as above.  out[nclosed,Hkv,D] bits. */
 void oracle_decode_means(const uint16_t* k, int dtype, int L, int Hkv, int D, int C,
                          uint16_t* out) {
   int nclosed = L / C;
   for (int c = 0; c < nclosed; ++c)
     for (int h = 0; h < Hkv; ++h)
       for (int d = 0; d < D; ++d) {
-        float acc = 0.0f;
-        for (int t = 0; t < C; ++t) acc = acc + to_f32(k[((size_t)(c * C + t) * Hkv + h) * D + d], dtype);
+        float acc;
+        CANON_SUM(C, to_f32(k[((size_t)(c * C + t) * Hkv + h) * D + d], dtype), acc);
         out[((size_t)c * Hkv + h) * D + d] = from_f32(acc / (float)C, dtype);
       }
 }

@@ -76,24 +76,38 @@ def test_calc_chunks_closed_form(lens, C):
 
 # ---------------------------------------------------------------- routing
 
+def _canon_sum(x):
+    """Independent numpy restatement of the canonical order: 64 strided fp32
+    partial sums, then the fixed pairwise tree (off = 32, 16, ..., 1)."""
+    part = np.zeros((64,) + x.shape[1:], np.float32)
+    for j in range(64):
+        acc = np.zeros(x.shape[1:], np.float32)
+        for t in range(j, x.shape[0], 64):
+            acc = (acc + x[t]).astype(np.float32)
+        part[j] = acc
+    off = 32
+    while off:
+        part[:off] = (part[:off] + part[off:2 * off]).astype(np.float32)
+        off //= 2
+    return part[0]
+
+
 @pytest.mark.parametrize("precision", [0, 1])
-def test_chunk_means_sequential_order(precision):
+@pytest.mark.parametrize("C", [8, 70, 200])
+def test_chunk_means_canonical_order(precision, C):
     torch.manual_seed(3)
-    k = torch.randn(40, 2, 8).bfloat16()
-    cu_chunk, _, filtered = O.calc_chunks([0, 40], 8)
-    m = O.chunk_means(O.bits16(k), 0, cu_chunk, filtered, 8, precision)
+    k = torch.randn(3 * C + 5, 2, 8).bfloat16()
+    cu_chunk, _, filtered = O.calc_chunks([0, k.shape[0]], C)
+    m = O.chunk_means(O.bits16(k), 0, cu_chunk, filtered, C, precision)
     kf = k.float().numpy()
     for f, c in enumerate(filtered):
-        acc = np.zeros((2, 8), np.float32)
-        for t in range(8):
-            acc = (acc + kf[cu_chunk[c] + t]).astype(np.float32)
-        want = (acc / np.float32(8)).astype(np.float32)
+        want = (_canon_sum(kf[cu_chunk[c]:cu_chunk[c] + C]) / np.float32(C)).astype(np.float32)
         if precision == 0:
             want = torch.from_numpy(want).bfloat16().float().numpy()
         np.testing.assert_array_equal(m[f].view(np.uint32), want.view(np.uint32))
-    # and it is the mean to within one rounding of the dtype
-    exact = kf[:32].reshape(4, 8, 2, 8).astype(np.float64).mean(1)
-    assert np.abs(m - exact).max() <= 2 ** -7 * np.abs(exact).max() + 1e-6
+    # and it is the mean to within about one rounding of the dtype
+    exact = kf[:3 * C].reshape(3, C, 2, 8).astype(np.float64).mean(1)
+    assert np.abs(m - exact).max() <= 2 ** -7 * np.abs(exact).max() + 1e-5
 
 
 def test_route_prefill_brute_force():
