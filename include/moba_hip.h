@@ -109,8 +109,10 @@ int moba_hip_prefill_bwd(const void* q, const void* k, const void* v, const void
 
 /* ----------------------------------------------------------------- decode */
 
-/* Tokens per paged_attention work item (sizes the split-K partial buffers). */
-int moba_hip_decode_sub_tokens(void);
+/* Number of work-list entries decode_route emits per (query, kv head, block
+ * of 16 q heads): (Hq / Hkv) * nslot.  Each entry is 16 bytes (int4: chunk,
+ * head mask, 4-bit slot indices of heads 0-7, of heads 8-15). */
+int moba_hip_decode_work_items(int Hq, int Hkv, int nslot);
 
 /* Scatter N new tokens k/v [N,Hkv,D] into the page pool
  * k_cache/v_cache [num_pages, page_size, Hkv, D] at (token_seq[n], token_pos[n])
@@ -136,30 +138,34 @@ int moba_hip_block_means(const void* k_cache, int dtype, int Hkv, int D, int pag
 /* Route of decode queries q [Nq,Hq,D]: fp32 fma-chain scores against the means
  * of the closed chunks c with (c+1)*chunk <= pos, stable top-R (descending,
  * ties -> lowest chunk).  selected [Nq,Hq,1+R]: slot 0 = pos / chunk, then the
- * chosen chunks, -1 padded.  scores [Nq,Hq,width] (required when R > 0;
- * -inf for illegal chunks).  Canonical fp32 means: see moba_hip_block_means.
+ * chosen chunks, -1 padded.  scores [Nq,Hq,width] (required when R > 0; -inf
+ * for illegal chunks; width <= 8192).  work_items (nullable)
+ * [Nq*Hkv*ceil(G/16), moba_hip_decode_work_items(Hq,Hkv,R+1)] int4 and
+ * work_counts [Nq*Hkv*ceil(G/16)]: per 16-head block the union of the chosen
+ * chunks for paged_attention.  At most 64 q heads per kv head.
  * Replaces _route_kernel + torch.topk / _stable_topk + _selected
  * (paged_decode.py:47-64, src/moba_opt/kv_cache.py:208-223,
  * prepared_decode.py:44-88). */
 int moba_hip_decode_route(const void* q, int dtype, int Nq, int Hq, int Hkv, int D,
                           const void* means, int max_chunks, const int* q_seq, const int* q_pos,
                           int chunk, int width, int R, float* scores, int* selected,
-                          void* stream);
+                          void* work_items, int* work_counts, void* stream);
 
 /* Paged attention of q [Nq,Hq,D] over the selected chunks (selected
- * [Nq,Hq,nslot]) or, with dense != 0, over every token <= pos; tokens are read
- * through the page table, each selected page once per KV-head group.
- * max_chunks_bound (dense) bounds pos / chunk + 1.  part_o
- * [Nq*Hq*S*nsub, D] and part_ml [Nq*Hq*S*nsub, 2] (S = nslot, or
- * max_chunks_bound when dense; nsub = ceil(chunk / moba_hip_decode_sub_tokens()))
- * are workspaces.  out [Nq,Hq,D] (dtype), lse [Nq,Hq] fp32 natural log.
+ * [Nq,Hq,nslot] + the route work list) or, with dense != 0, over every token
+ * <= pos; tokens are read through the page table, each selected page once per
+ * 16-head block of a KV-head group.  max_chunks_bound (dense) bounds
+ * pos / chunk + 1.  part_o [Nq*Hq*S, D] and part_ml [Nq*Hq*S, 2] fp32
+ * (S = nslot, or max_chunks_bound when dense) are workspaces.
+ * out [Nq,Hq,D] (dtype), lse [Nq,Hq] fp32 natural log.
  * Replaces _attention_kernel (paged_decode.py:67-112). */
 int moba_hip_paged_attention(const void* q, int dtype, int Nq, int Hq, int Hkv, int D,
                              const void* k_cache, const void* v_cache, int page_size,
                              const int* table, int table_width, const int* lengths,
                              const int* q_seq, const int* q_pos, const int* selected, int nslot,
-                             int dense, int chunk, int max_chunks_bound, float* part_o,
-                             float* part_ml, void* out, float* lse, void* stream);
+                             const void* work_items, const int* work_counts, int dense,
+                             int chunk, int max_chunks_bound, float* part_o, float* part_ml,
+                             void* out, float* lse, void* stream);
 
 /* Prepared-decode metadata step for B fixed rows: apply the page-table delta
  * [2,B] (logical, physical; -1 = none), write positions = lengths (append) or
@@ -167,6 +173,17 @@ int moba_hip_paged_attention(const void* q, int dtype, int Nq, int Hq, int Hkv, 
  * Replaces _metadata (prepared_decode.py:6-20). */
 int moba_hip_decode_metadata(int* table, int table_width, int* lengths, const int* ids,
                              int* positions, const int* delta, int B, int append, void* stream);
+
+/* Prepared-decode step prologue in ONE launch for B fixed rows: apply the
+ * page-table delta, positions = lengths, lengths += 1, scatter the new token
+ * k/v [B,Hkv,D] into the pool, and, for a row whose token closes its chunk,
+ * write that chunk's mean (same canonical order as moba_hip_block_means).
+ * Replaces _metadata + _append_kernel + _step_means
+ * (prepared_decode.py:6-41, paged_decode.py:10-23). */
+int moba_hip_decode_step(int* table, int table_width, int* lengths, const int* ids,
+                         int* positions, const int* delta, int B, const void* k, const void* v,
+                         int dtype, void* k_cache, void* v_cache, int page_size, int Hkv, int D,
+                         int chunk, void* means, int max_chunks, void* stream);
 
 #ifdef __cplusplus
 }

@@ -14,13 +14,20 @@
 //                       table (_attention_kernel), then a deterministic combine
 //   decode_metadata   : page-table delta, positions, length advance (_metadata)
 //
-// paged_attention: one wave per (query, kv head, 16-head block, chunk of the
-// union of the group's selections, sub-block of <= kSub tokens).  Each
-// selected page is read once for all the q heads of the group.  Scores are
-// S^T = K Q^T on v_mfma_f32_16x16x32 (16 tokens x 16 heads, K read straight
-// from the pool), O^T += V^T P^T with V^T taken from a row-major LDS tile by
-// the transposed LDS read.  Partials (o, max, sum) per (query, head, slot,
-// sub-block) are merged in a fixed order by combine_kernel.
+//   decode_step       : prepared-decode step prologue in one launch: page-table
+//                       delta + positions + length advance, the scatter of the
+//                       new token, and the mean of a chunk the token closes
+//
+// decode_route builds, per (query, kv head, block of 16 q heads), a work list:
+// the union of the chunks the heads selected (first-occurrence order), each
+// with the mask of heads that chose it and their slot indices.
+// paged_attention runs one 8-wave workgroup per work item (one whole chunk):
+// every selected page is read once for all the q heads of the group.  Scores
+// are S^T = K Q^T on v_mfma_f32_16x16x32 (16 tokens x 16 heads, K straight from
+// the pool), O^T += V^T P^T with V^T taken from a row-major LDS tile by the
+// transposed LDS read.  The waves split the chunk's tokens and merge in LDS;
+// partials (o, max, sum) per (query, head, slot) are merged in slot order by
+// combine_kernel.
 #include "common.h"
 #include "../../include/moba_hip.h"
 
@@ -40,7 +47,7 @@ MOBA_DEV f32x4v mfma16(const u16x8_t& a, const u16x8_t& b, const f32x4v& c) {
                                                   __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
 }
 
-constexpr int kSub = 128;  // tokens per attention work item
+constexpr int kWaves = 8;  // waves per attention workgroup
 constexpr int kMaxRemote = 8;
 
 // ------------------------------------------------------------------ append
@@ -137,58 +144,157 @@ __global__ __launch_bounds__(64) void means_kernel(const uint16_t* __restrict__ 
 }
 
 // ------------------------------------------------------------------- route
-// One wave per (query row, q head).  Lane j scores chunks j, j+64, ... (fp32
-// fma chain over d, the canonical gate order) against the cache-dtype means;
-// the stable top-R is R rounds of a wave argmax: each round takes the best
+// One workgroup (4 waves) per (query row, kv head).  Wave w scores the heads
+// g = w, w+4, ... of the group: lane j takes chunks j, j+64, ... (fp32 fma
+// chain over d, the canonical gate order) against the cache-dtype means; the
+// stable top-R is R rounds of a wave argmax, each round taking the best
 // candidate strictly after the previous pick in (score desc, chunk asc) order.
-template <int DT>
-__global__ __launch_bounds__(64) void route_kernel(const uint16_t* __restrict__ q, int Hq, int Hkv,
-                                                   int D, const uint16_t* __restrict__ means,
-                                                   int max_chunks, const int* __restrict__ seq,
-                                                   const int* __restrict__ pos, int C, int width,
-                                                   int R, float* __restrict__ scores,
-                                                   int* __restrict__ selected) {
-  __shared__ float qs[256];
-  const int idx = blockIdx.x;  // row * Hq + h
-  const int row = idx / Hq, h = idx % Hq;
-  const int kh = h / (Hq / Hkv);
-  const int lane = threadIdx.x;
-  const int sid = seq[row], p = pos[row];
-  for (int d = lane; d < D; d += 64) qs[d] = to_f32<DT>(q[(int64_t)idx * D + d]);
-  __syncthreads();
+// Thread 0 then writes the work list of every 16-head block.
+struct WorkItem {
+  int chunk, mask, slots_lo, slots_hi;  // slots: 4 bits per head of the block
+};
+
+template <int DT, int DP, bool VEC>
+__global__ __launch_bounds__(1024) void route_kernel(const uint16_t* __restrict__ q, int Hq, int Hkv,
+                                                     int D, const uint16_t* __restrict__ means,
+                                                     int max_chunks, const int* __restrict__ seq,
+                                                     const int* __restrict__ pos, int C, int width,
+                                                     int R, float* __restrict__ scores,
+                                                     int* __restrict__ selected,
+                                                     WorkItem* __restrict__ items,
+                                                     int* __restrict__ item_counts, int max_items) {
+  extern __shared__ float sc_lds[];  // [waves][width]
+  __shared__ int sel_s[64 * 9];
+  __shared__ int first_s[16 * 9], rank_s[16 * 9];
+  __shared__ WorkItem it_s[16 * 9];
+  __shared__ int n_s;
+  const int G = Hq / Hkv, NHB = (G + 15) / 16;
+  const int nw = blockDim.x >> 6;
+  const int qrow = blockIdx.x / Hkv, kh = blockIdx.x % Hkv;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int sid = seq[qrow], p = pos[qrow];
   const int legal = min(p / C, width);  // chunks c with (c+1)*C <= p
-  float* srow = scores + (int64_t)idx * width;
-  for (int c = lane; c < width; c += 64) {
-    float acc = -INFINITY;
-    if (c < legal) {
-      const uint16_t* mr = means + (((int64_t)sid * max_chunks + c) * Hkv + kh) * D;
-      acc = 0.0f;
-      for (int d = 0; d < D; ++d) acc = fmaf(to_f32<DT>(mr[d]), qs[d], acc);
-    }
-    srow[c] = acc;
-  }
-  __syncthreads();  // scores of this row are re-read by other lanes below
-  int* out = selected + (int64_t)idx * (R + 1);
-  if (lane == 0) out[0] = p / C;
-  float last_v = INFINITY;
-  int last_c = -1;
-  for (int r = 0; r < R; ++r) {
-    float bv = -INFINITY;
-    int bc = 0x7fffffff;
-    for (int c = lane; c < legal; c += 64) {
-      const float v = srow[c];
-      const bool after = v < last_v || (v == last_v && c > last_c);
-      if (after && (v > bv || (v == bv && c < bc))) { bv = v; bc = c; }
-    }
+  float* sc = sc_lds + w * width;
+  for (int g0 = 0; g0 < G; g0 += nw) {
+    const int g = g0 + w;
+    if (g < G) {
+      const int h = kh * G + g;
+      const int64_t idx = (int64_t)qrow * Hq + h;
+      const uint16_t* qr = q + idx * D;
+      if constexpr (VEC) {
+        // the whole q row in registers; every means row loaded in one burst
+        u16x8_t qv[DP / 8];
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      const float ov = __shfl_xor(bv, off, 64);
-      const int oc = __shfl_xor(bc, off, 64);
-      if (ov > bv || (ov == bv && oc < bc)) { bv = ov; bc = oc; }
+        for (int x = 0; x < DP / 8; ++x) qv[x] = x * 8 < D ? ld8(qr + x * 8) : zero8();
+        for (int c = lane; c < width; c += 64) {
+          float acc = -INFINITY;
+          if (c < legal) {
+            const uint16_t* mr = means + (((int64_t)sid * max_chunks + c) * Hkv + kh) * D;
+            u16x8_t mv[DP / 8];
+#pragma unroll
+            for (int x = 0; x < DP / 8; ++x) mv[x] = x * 8 < D ? ld8(mr + x * 8) : zero8();
+            acc = 0.0f;
+#pragma unroll
+            for (int x = 0; x < DP / 8; ++x)
+              if (x * 8 < D) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                  acc = fmaf(to_f32<DT>(mv[x][e]), to_f32<DT>(qv[x][e]), acc);
+              }
+          }
+          sc[c] = acc;
+          scores[idx * width + c] = acc;
+        }
+      } else {
+        for (int c = lane; c < width; c += 64) {
+          float acc = -INFINITY;
+          if (c < legal) {
+            const uint16_t* mr = means + (((int64_t)sid * max_chunks + c) * Hkv + kh) * D;
+            acc = 0.0f;
+            for (int d = 0; d < D; ++d) acc = fmaf(to_f32<DT>(mr[d]), to_f32<DT>(qr[d]), acc);
+          }
+          sc[c] = acc;
+          scores[idx * width + c] = acc;
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      int* out = selected + idx * (R + 1);
+      if (lane == 0) { out[0] = p / C; sel_s[g * (R + 1)] = p / C; }
+      float last_v = INFINITY;
+      int last_c = -1;
+      for (int r = 0; r < R; ++r) {
+        float bv = -INFINITY;
+        int bc = 0x7fffffff;
+        for (int c = lane; c < legal; c += 64) {
+          const float v = sc[c];
+          const bool after = v < last_v || (v == last_v && c > last_c);
+          if (after && (v > bv || (v == bv && c < bc))) { bv = v; bc = c; }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+          const float ov = __shfl_xor(bv, off, 64);
+          const int oc = __shfl_xor(bc, off, 64);
+          if (ov > bv || (ov == bv && oc < bc)) { bv = ov; bc = oc; }
+        }
+        const bool found = bv > -INFINITY;
+        if (lane == 0) {
+          out[1 + r] = found ? bc : -1;
+          sel_s[g * (R + 1) + 1 + r] = found ? bc : -1;
+        }
+        if (found) { last_v = bv; last_c = bc; } else { last_v = -INFINITY; last_c = 0x7fffffff; }
+      }
     }
-    const bool found = bv > -INFINITY;
-    if (lane == 0) out[1 + r] = found ? bc : -1;
-    if (found) { last_v = bv; last_c = bc; } else { last_v = -INFINITY; last_c = 0x7fffffff; }
+    __syncthreads();  // the wave's score buffer is reused by its next head
+  }
+  if (items == nullptr) return;
+  // Work list of each 16-head block: distinct chunks in first-occurrence
+  // order over the flattened (head, slot) entries, with the mask of heads that
+  // chose each chunk and their slot indices.  Built in parallel: entry e finds
+  // its first occurrence by comparison, ranks come from a ballot prefix count.
+  const int S = R + 1;
+  for (int hb = 0; hb < NHB; ++hb) {
+    const int g_lo = hb * 16, ng = min(16, G - g_lo), E = ng * S;
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+      const int c = sel_s[g_lo * S + e];
+      int first = -1;
+      if (c >= 0) {
+        first = e;
+        for (int e2 = 0; e2 < e; ++e2)
+          if (sel_s[g_lo * S + e2] == c) { first = e2; break; }
+      }
+      first_s[e] = first;
+      it_s[e].chunk = 0; it_s[e].mask = 0; it_s[e].slots_lo = 0; it_s[e].slots_hi = 0;
+    }
+    __syncthreads();
+    if (w == 0) {
+      int base = 0;
+      for (int e0 = 0; e0 < E; e0 += 64) {
+        const int e = e0 + lane;
+        const bool is_first = e < E && first_s[e] == e;
+        const uint64_t m = __ballot(is_first);
+        if (e < E) rank_s[e] = base + __popcll(m & ((1ull << lane) - 1ull));
+        base += __popcll(m);
+      }
+      if (lane == 0) n_s = base;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+      const int f = first_s[e];
+      if (f < 0) continue;
+      const int x = rank_s[f], b = e / S, j = e % S;
+      if (f == e) it_s[x].chunk = sel_s[g_lo * S + e];
+      atomicOr(&it_s[x].mask, 1 << b);
+      if (b < 8) atomicOr(&it_s[x].slots_lo, j << (4 * b));
+      else atomicOr(&it_s[x].slots_hi, j << (4 * (b - 8)));
+    }
+    __syncthreads();
+    const int n = n_s;
+    WorkItem* it = items + ((int64_t)blockIdx.x * NHB + hb) * max_items;
+    for (int x = threadIdx.x; x < n; x += blockDim.x) it[x] = it_s[x];
+    if (threadIdx.x == 0) item_counts[blockIdx.x * NHB + hb] = n;
+    __syncthreads();
   }
 }
 
@@ -198,65 +304,61 @@ struct AttnArgs {
   const uint16_t* kc;
   const uint16_t* vc;
   int Nq, Hq, Hkv, D, G, NHB;
-  int P, W, C, nslot, nsub, dense;
+  int P, W, C, nslot, dense, max_items;
   float scale_log2;
   const int* table;
   const int* lengths;
   const int* seq;
   const int* pos;
   const int* selected;
+  const WorkItem* items;
+  const int* item_counts;
   float* part_o;
   float* part_ml;
   uint16_t* out;
   float* lse;
 };
 
-// Token range of (chunk c, sub-block b) for a query at p over a sequence of
-// length len; empty when t0 >= t1.
-MOBA_DEV void sub_range(int c, int b, int C, int p, int len, int& t0, int& t1) {
-  t0 = c * C + b * kSub;
-  t1 = min(min(t0 + kSub, (c + 1) * C), min(p + 1, len));
-}
-
 template <int DT, int DP, bool VEC>
-__global__ __launch_bounds__(64) void attn_kernel(AttnArgs a) {
+__global__ __launch_bounds__(512) void attn_kernel(AttnArgs a) {
   constexpr int NKS = DP / 32;  // 32-d k-steps of S^T
   constexpr int NDB = DP / 16;  // 16-d blocks of O^T
   constexpr int VS = DP + 8;
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[32 * VS];
+  constexpr int STAGE = 32 * VS;  // per-wave V tile (elements)
+  constexpr int STAGE_BYTES = kWaves * STAGE * 2;
+  constexpr int MERGE_BYTES = kWaves * (16 * DP + 32) * 4;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[STAGE_BYTES > MERGE_BYTES ? STAGE_BYTES : MERGE_BYTES];
+  uint16_t* Vs = reinterpret_cast<uint16_t*>(lds) + (threadIdx.x >> 6) * STAGE;
 
-  const int lane = threadIdx.x, g4 = lane >> 4, c16 = lane & 15;
-  const int bx = blockIdx.x;
-  const int qrow = bx / (a.Hkv * a.NHB), kh = (bx / a.NHB) % a.Hkv, hb = bx % a.NHB;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g4 = lane >> 4, c16 = lane & 15;
+  const int r = blockIdx.x;  // (qrow * Hkv + kh) * NHB + hb
+  const int hb = r % a.NHB, kh = (r / a.NHB) % a.Hkv, qrow = r / (a.NHB * a.Hkv);
   const int G = a.G, D = a.D;
-  const int sid = a.seq[qrow], p = a.pos[qrow], len = a.lengths[sid];
-  const int u = blockIdx.y, b = blockIdx.z;
-  const int hg = hb * 16 + c16;  // this lane's head within the group
-  const int h = kh * G + hg;
-  const bool head_ok = hg < G;
-
-  int c, jh = -1;
+  const int p = a.pos[qrow];
+  const int n_items = a.dense ? p / a.C + 1 : a.item_counts[r];
+  if ((int)blockIdx.y >= n_items) return;
+  const int sid = a.seq[qrow], len = a.lengths[sid];
+  // the workgroup takes work items blockIdx.y, blockIdx.y + gridDim.y, ...
+  for (int i = blockIdx.y; i < n_items; i += gridDim.y) {
+  int c, mask, jh = -1;
   if (a.dense) {
-    c = u;
-    if (c > p / a.C) return;
-    jh = head_ok ? c : -1;
+    c = i;
+    const int nh = min(16, G - hb * 16);
+    mask = (int)((1u << nh) - 1u);
+    jh = c;
   } else {
-    const int* sel = a.selected + ((int64_t)qrow * a.Hq + kh * G) * a.nslot;
-    const int gu = u / a.nslot, ju = u % a.nslot;
-    c = sel[gu * a.nslot + ju];
-    if (c < 0) return;
-    for (int x = 0; x < gu * a.nslot + ju; ++x)  // first occurrence in the union only
-      if (sel[x] == c) return;
-    if (head_ok)
-      for (int j = 0; j < a.nslot; ++j)
-        if (sel[hg * a.nslot + j] == c) { jh = j; break; }
+    const WorkItem it = a.items[(int64_t)r * a.max_items + i];
+    c = it.chunk;
+    mask = it.mask;
+    jh = c16 < 8 ? (it.slots_lo >> (4 * c16)) & 15 : (it.slots_hi >> (4 * (c16 - 8))) & 15;
   }
-  if (__ballot(jh >= 0) == 0) return;
-  int t0, t1;
-  sub_range(c, b, a.C, p, len, t0, t1);
-  if (t0 >= t1) return;
-
+  const bool head_on = (mask >> c16) & 1;
+  const int hg = hb * 16 + c16;
+  const int h = kh * G + hg;
+  const int t_begin = c * a.C;
+  const int t_end = min(min((c + 1) * a.C, p + 1), len);
   const int* trow = a.table + (int64_t)sid * a.W;
+
   u16x8_t qf[NKS];
   {
     const uint16_t* qp = a.q + ((int64_t)qrow * a.Hq + h) * D;
@@ -264,10 +366,10 @@ __global__ __launch_bounds__(64) void attn_kernel(AttnArgs a) {
     for (int ks = 0; ks < NKS; ++ks) {
       const int d = ks * 32 + g4 * 8;
       if constexpr (VEC) {
-        qf[ks] = (head_ok && d < D) ? ld8(qp + d) : zero8();
+        qf[ks] = (head_on && d < D) ? ld8(qp + d) : zero8();
       } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) qf[ks][e] = (head_ok && d + e < D) ? qp[d + e] : (uint16_t)0;
+        for (int e = 0; e < 8; ++e) qf[ks][e] = (head_on && d + e < D) ? qp[d + e] : (uint16_t)0;
       }
     }
   }
@@ -276,37 +378,54 @@ __global__ __launch_bounds__(64) void attn_kernel(AttnArgs a) {
   for (int db = 0; db < NDB; ++db) oacc[db] = (f32x4v){0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, lsum = 0.0f;
 
-  for (int tt = t0; tt < t1; tt += 32) {
-    // K rows of the two 16-token tiles (A operand, straight from the pool)
-    f32x4v sc[2];
+  // wave w takes the 32-token steps w, w + 8, ... of the chunk; the K rows and
+  // V rows of the next step are loaded into registers while this one computes
+  constexpr int VLD = 32 * (DP / 8) / 64;  // 16-byte V chunks per lane per step
+  constexpr bool PREFETCH = DP <= 128;
+  // Page of token t0 + r (0 <= r < 32) from one division per step: pages of at
+  // least 32 tokens hold the step in at most two pages.
+  auto page_of = [&](int t0, int pg0, int off0, int r) -> int {
+    const int tok = t0 + r;
+    if (tok >= t_end) return -1;
+    int off = off0 + r, pg = pg0;
+    if (off >= a.P) {
+      if (a.P >= 32) { pg += 1; } else { pg += off / a.P; }
+    }
+    return trow[pg];
+  };
+  auto tok_off = [&](int off0, int r) -> int {  // row of token t0 + r inside its page
+    const int off = off0 + r;
+    return off < a.P ? off : (a.P >= 32 ? off - a.P : off % a.P);
+  };
+  auto load = [&](int t0, u16x8_t (&kr)[2][NKS], u16x8_t (&vr)[VLD]) {
+    const int pg0 = t0 / a.P, off0 = t0 - pg0 * a.P;
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
-      const int tok = tt + half * 16 + c16;
-      const int page = tok < t1 ? trow[tok / a.P] : -1;
+      const int tok = t0 + half * 16 + c16;
+      const int page = page_of(t0, pg0, off0, half * 16 + c16);
       const bool tok_ok = page >= 0;  // unmapped pages read as zero, never out of the pool
-      const int64_t base = tok_ok ? (((int64_t)page * a.P + tok % a.P) * a.Hkv + kh) * D : 0;
-      sc[half] = (f32x4v){0.f, 0.f, 0.f, 0.f};
+      const int64_t base =
+          tok_ok ? (((int64_t)page * a.P + tok_off(off0, half * 16 + c16)) * a.Hkv + kh) * D : 0;
+      (void)tok;
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {
         const int d = ks * 32 + g4 * 8;
-        u16x8_t kv;
         if constexpr (VEC) {
-          kv = (tok_ok && d < D) ? ld8(a.kc + base + d) : zero8();
+          kr[half][ks] = (tok_ok && d < D) ? ld8(a.kc + base + d) : zero8();
         } else {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) kv[e] = (tok_ok && d + e < D) ? a.kc[base + d + e] : (uint16_t)0;
+          for (int e = 0; e < 8; ++e)
+            kr[half][ks][e] = (tok_ok && d + e < D) ? a.kc[base + d + e] : (uint16_t)0;
         }
-        sc[half] = mfma16<DT>(kv, qf[ks], sc[half]);
       }
     }
-    // stage the V rows of these 32 tokens (row-major) for the transposed read
-    for (int id = lane; id < 32 * (DP / 8); id += 64) {
-      const int r = id / (DP / 8), dc = (id % (DP / 8)) * 8;
-      const int tok = tt + r;
+#pragma unroll
+    for (int x = 0; x < VLD; ++x) {
+      const int id = lane + 64 * x, rr = id / (DP / 8), dc = (id % (DP / 8)) * 8;
+      const int page = page_of(t0, pg0, off0, rr);
       u16x8_t vv = zero8();
-      const int page = tok < t1 ? trow[tok / a.P] : -1;
       if (page >= 0) {
-        const int64_t base = (((int64_t)page * a.P + tok % a.P) * a.Hkv + kh) * D;
+        const int64_t base = (((int64_t)page * a.P + tok_off(off0, rr)) * a.Hkv + kh) * D;
         if constexpr (VEC) {
           if (dc < D) vv = ld8(a.vc + base + dc);
         } else {
@@ -314,18 +433,31 @@ __global__ __launch_bounds__(64) void attn_kernel(AttnArgs a) {
           for (int e = 0; e < 8; ++e) vv[e] = dc + e < D ? a.vc[base + dc + e] : (uint16_t)0;
         }
       }
-      st8(&Vs[r * VS + dc], vv);
+      vr[x] = vv;
     }
-    // online softmax for this lane's head over tokens {4g4+i, 16+4g4+i}
+  };
+  auto compute = [&](int tt, const u16x8_t (&kr)[2][NKS], const u16x8_t (&vr)[VLD]) {
+    f32x4v sc[2];
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      sc[half] = (f32x4v){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) sc[half] = mfma16<DT>(kr[half][ks], qf[ks], sc[half]);
+    }
+#pragma unroll
+    for (int x = 0; x < VLD; ++x) {
+      const int id = lane + 64 * x, rr = id / (DP / 8), dc = (id % (DP / 8)) * 8;
+      st8(&Vs[rr * VS + dc], vr[x]);
+    }
     float mx = -INFINITY;
 #pragma unroll
     for (int half = 0; half < 2; ++half)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int tok = tt + half * 16 + 4 * g4 + i;
-        const float x = tok < t1 ? sc[half][i] * a.scale_log2 : -INFINITY;
-        sc[half][i] = x;
-        mx = fmaxf(mx, x);
+      for (int e = 0; e < 4; ++e) {
+        const int tok = tt + half * 16 + 4 * g4 + e;
+        const float xv = tok < t_end ? sc[half][e] * a.scale_log2 : -INFINITY;
+        sc[half][e] = xv;
+        mx = fmaxf(mx, xv);
       }
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
@@ -334,16 +466,19 @@ __global__ __launch_bounds__(64) void attn_kernel(AttnArgs a) {
     m_run = mn;
     float pr[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      pr[i] = fast_exp2(sc[0][i] - mn);
-      pr[4 + i] = fast_exp2(sc[1][i] - mn);
+    for (int e = 0; e < 4; ++e) {
+      pr[e] = fast_exp2(sc[0][e] - mn);
+      pr[4 + e] = fast_exp2(sc[1][e] - mn);
     }
     float ps = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) ps += pr[e];
     lsum = lsum * alpha + ps;
     const u16x8_t pv = pack8<DT>(pr);
-    __syncthreads();
+    // the V tile is private to this wave: order its LDS stores before the reads
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
       // A = V^T (16 d x 32 tokens): column db*16 + c16, rows 4g4.. and 16+4g4..
@@ -353,75 +488,114 @@ __global__ __launch_bounds__(64) void attn_kernel(AttnArgs a) {
       av[0] = lo[0]; av[1] = lo[1]; av[2] = lo[2]; av[3] = lo[3];
       av[4] = hi[0]; av[5] = hi[1]; av[6] = hi[2]; av[7] = hi[3];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) oacc[db][i] *= alpha;
+      for (int e = 0; e < 4; ++e) oacc[db][e] *= alpha;
       oacc[db] = mfma16<DT>(av, pv, oacc[db]);
     }
-    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  constexpr int kStride = 32 * kWaves;
+  int tt = t_begin + 32 * w;
+  if (tt < t_end) {
+    u16x8_t kr[2][NKS], vr[VLD];
+    load(tt, kr, vr);
+    if constexpr (PREFETCH) {
+      for (; tt + kStride < t_end; tt += kStride) {
+        u16x8_t kn[2][NKS], vn[VLD];
+        load(tt + kStride, kn, vn);
+        compute(tt, kr, vr);
+#pragma unroll
+        for (int half = 0; half < 2; ++half)
+#pragma unroll
+          for (int ks = 0; ks < NKS; ++ks) kr[half][ks] = kn[half][ks];
+#pragma unroll
+        for (int x = 0; x < VLD; ++x) vr[x] = vn[x];
+      }
+      compute(tt, kr, vr);
+    } else {
+      for (;;) {
+        compute(tt, kr, vr);
+        tt += kStride;
+        if (tt >= t_end) break;
+        load(tt, kr, vr);
+      }
+    }
   }
   lsum += __shfl_xor(lsum, 16, 64);
   lsum += __shfl_xor(lsum, 32, 64);
-  if (jh < 0) return;
-  const int64_t entry = (((int64_t)qrow * a.Hq + h) * a.nslot + jh) * a.nsub + b;
-  const float inv = 1.0f / lsum;
-  float* po = a.part_o + entry * D;
+
+  // merge the waves in LDS: per wave [16 heads][DP] of O^T plus (m, l) per head
+  __shared__ int slot_s[16];
+  if (tid < 16) slot_s[tid] = jh;  // lanes 0..15 of wave 0 hold heads 0..15
+  __syncthreads();
+  float* mrg = reinterpret_cast<float*>(lds);
+  float* wo = mrg + w * (16 * DP + 32);
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int d = db * 16 + 4 * g4 + i;
-      if (d < D) po[d] = oacc[db][i] * inv;
+    for (int e = 0; e < 4; ++e) wo[c16 * DP + db * 16 + 4 * g4 + e] = oacc[db][e];
+  if (g4 == 0) { wo[16 * DP + c16] = m_run; wo[16 * DP + 16 + c16] = lsum; }
+  __syncthreads();
+  for (int x = tid; x < 16 * DP; x += 512) {
+    const int hh = x / DP, d = x % DP;
+    if (!((mask >> hh) & 1) || d >= D) continue;
+    float M = -INFINITY;
+    for (int ww = 0; ww < kWaves; ++ww) {
+      const float* o = mrg + ww * (16 * DP + 32);
+      if (o[16 * DP + 16 + hh] > 0.0f) M = fmaxf(M, o[16 * DP + hh]);
     }
-  if (g4 == 0) {  // (max, sum) in the log2 domain: exact to merge at any magnitude
-    a.part_ml[2 * entry] = m_run;
-    a.part_ml[2 * entry + 1] = lsum;
+    float z = 0.0f, acc = 0.0f;
+    for (int ww = 0; ww < kWaves; ++ww) {
+      const float* o = mrg + ww * (16 * DP + 32);
+      const float l = o[16 * DP + 16 + hh];
+      if (l > 0.0f) {
+        const float f = fast_exp2(o[16 * DP + hh] - M);
+        z += l * f;
+        acc += o[hh * DP + d] * f;
+      }
+    }
+    const int hj = hb * 16 + hh;
+    const int j = slot_s[hh];
+    const int64_t entry = ((int64_t)qrow * a.Hq + kh * G + hj) * a.nslot + j;
+    a.part_o[entry * D + d] = acc / z;
+    if (d == 0) { a.part_ml[2 * entry] = M; a.part_ml[2 * entry + 1] = z; }
+  }
+  __syncthreads();  // the merge buffer aliases the V tiles of the next item
   }
 }
 
-// One wave per (query, head): merge the partials of every slot / sub-block
-// in ascending order.
+// One wave per (query, head): merge the per-slot partials in slot order.
 template <int DT>
 __global__ __launch_bounds__(64) void combine_kernel(AttnArgs a) {
   const int row = blockIdx.x;  // qrow * Hq + h
   const int qrow = row / a.Hq;
   const int lane = threadIdx.x, D = a.D;
-  const int sid = a.seq[qrow], p = a.pos[qrow], len = a.lengths[sid];
+  const int p = a.pos[qrow];
   const int* sel = a.selected + (int64_t)row * a.nslot;
   const int nj = a.dense ? p / a.C + 1 : a.nslot;
   float M = -INFINITY;
-  for (int j = 0; j < nj; ++j) {
-    const int c = a.dense ? j : sel[j];
-    if (c < 0) continue;
-    for (int b = 0; b < a.nsub; ++b) {
-      int t0, t1;
-      sub_range(c, b, a.C, p, len, t0, t1);
-      if (t0 < t1) M = fmaxf(M, a.part_ml[2 * (((int64_t)row * a.nslot + j) * a.nsub + b)]);
-    }
-  }
+  for (int j = 0; j < nj; ++j)
+    if (a.dense || sel[j] >= 0) M = fmaxf(M, a.part_ml[2 * ((int64_t)row * a.nslot + j)]);
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   float z = 0.0f;
   for (int j = 0; j < nj; ++j) {
-    const int c = a.dense ? j : sel[j];
-    if (c < 0) continue;
-    for (int b = 0; b < a.nsub; ++b) {
-      int t0, t1;
-      sub_range(c, b, a.C, p, len, t0, t1);
-      if (t0 >= t1) continue;
-      const int64_t entry = ((int64_t)row * a.nslot + j) * a.nsub + b;
-      const float w = a.part_ml[2 * entry + 1] * fast_exp2(a.part_ml[2 * entry] - M);
-      z += w;
-      const float* po = a.part_o + entry * D;
+    if (!a.dense && sel[j] < 0) continue;
+    const int64_t entry = (int64_t)row * a.nslot + j;
+    const float wgt = a.part_ml[2 * entry + 1] * fast_exp2(a.part_ml[2 * entry] - M);
+    z += wgt;
+    const float* po = a.part_o + entry * D;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int d = lane + 64 * i;
-        if (d < D) acc[i] += w * po[d];
-      }
+    for (int x = 0; x < 4; ++x) {
+      const int d = lane + 64 * x;
+      if (d < D) acc[x] += wgt * po[d];
     }
   }
   const float invz = 1.0f / z;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int d = lane + 64 * i;
-    if (d < D) a.out[(int64_t)row * D + d] = from_f32<DT>(acc[i] * invz);
+  for (int x = 0; x < 4; ++x) {
+    const int d = lane + 64 * x;
+    if (d < D) a.out[(int64_t)row * D + d] = from_f32<DT>(acc[x] * invz);
   }
   if (lane == 0) a.lse[row] = (M + log2f(z)) * kLn2;
 }
@@ -444,13 +618,86 @@ __global__ void metadata_kernel(int* __restrict__ table, int W, int* __restrict_
   }
 }
 
+// Prepared-decode step prologue, one workgroup per active row: page-table
+// delta, position / length advance, scatter of the new token, and, when the
+// token closes its chunk, that chunk's mean (canonical order, one wave per
+// (kv head, 8 d)).
+template <int DT>
+__global__ __launch_bounds__(256) void step_kernel(int* __restrict__ table, int W,
+                                                   int* __restrict__ lengths,
+                                                   const int* __restrict__ ids,
+                                                   int* __restrict__ positions,
+                                                   const int* __restrict__ delta, int B,
+                                                   const uint16_t* __restrict__ k,
+                                                   const uint16_t* __restrict__ v,
+                                                   uint16_t* __restrict__ kc,
+                                                   uint16_t* __restrict__ vc, int P, int Hkv,
+                                                   int D, int C, uint16_t* __restrict__ means,
+                                                   int max_chunks) {
+  __shared__ int s_pos, s_page;
+  const int row = blockIdx.x, tid = threadIdx.x;
+  const int sid = ids[row];
+  if (tid == 0) {
+    const int logical = delta[row], physical = delta[B + row];
+    if (logical >= 0) table[(int64_t)sid * W + logical] = physical;
+    const int length = lengths[sid];
+    positions[row] = length;
+    lengths[sid] = length + 1;
+    s_pos = length;
+    s_page = table[(int64_t)sid * W + length / P];
+  }
+  __syncthreads();
+  const int p = s_pos, page = s_page;
+  if (page >= 0) {
+    const int64_t dst = (((int64_t)page * P + p % P) * Hkv) * D;
+    const int64_t src = (int64_t)row * Hkv * D;
+    for (int x = tid; x < Hkv * D; x += 256) {
+      kc[dst + x] = k[src + x];
+      vc[dst + x] = v[src + x];
+    }
+  }
+  if ((p + 1) % C != 0) return;  // workgroup-uniform
+  __syncthreads();  // the token written above is part of the chunk mean
+  const int chunk = p / C, nd8 = (D + 7) / 8;
+  const int lane = tid & 63, w = tid >> 6;
+  const int* trow = table + (int64_t)sid * W;
+  for (int item = w; item < Hkv * nd8; item += 4) {
+    const int kh = item / nd8, d0 = (item % nd8) * 8;
+    float acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+    for (int t = chunk * C + lane; t < (chunk + 1) * C; t += 64) {
+      const int pg = trow[t / P];
+      if (pg < 0) continue;
+      const int64_t off = (((int64_t)pg * P + t % P) * Hkv + kh) * D + d0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (d0 + e < D) acc[e] = acc[e] + to_f32<DT>(kc[off + e]);
+    }
+    uint16_t res[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) res[e] = from_f32<DT>(canon_tree(acc[e]) / (float)C);
+    if (lane == 0) {
+      uint16_t* dstm = means + (((int64_t)sid * max_chunks + chunk) * Hkv + kh) * D + d0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (d0 + e < D) dstm[e] = res[e];
+    }
+  }
+}
+
 template <int DT, int DP>
 int launch_attn(const AttnArgs& a, int n_items, hipStream_t st) {
-  dim3 grid((unsigned)(a.Nq * a.Hkv * a.NHB), (unsigned)n_items, (unsigned)a.nsub);
+  // enough workgroups to fill the chip twice; each loops over its items
+  const int rows = a.Nq * a.Hkv * a.NHB;
+  int ny = (512 + rows - 1) / rows;
+  if (ny > n_items) ny = n_items;
+  if (ny < 1) ny = 1;
+  dim3 grid((unsigned)rows, (unsigned)ny);
   if (a.D % 8 == 0)
-    hipLaunchKernelGGL((attn_kernel<DT, DP, true>), grid, dim3(64), 0, st, a);
+    hipLaunchKernelGGL((attn_kernel<DT, DP, true>), grid, dim3(64 * kWaves), 0, st, a);
   else
-    hipLaunchKernelGGL((attn_kernel<DT, DP, false>), grid, dim3(64), 0, st, a);
+    hipLaunchKernelGGL((attn_kernel<DT, DP, false>), grid, dim3(64 * kWaves), 0, st, a);
   hipLaunchKernelGGL(combine_kernel<DT>, dim3((unsigned)(a.Nq * a.Hq)), dim3(64), 0, st, a);
   return moba_launch_status("paged_attention");
 }
@@ -465,7 +712,9 @@ int dispatch_attn(const AttnArgs& a, int n_items, hipStream_t st) {
 
 }  // namespace
 
-extern "C" int moba_hip_decode_sub_tokens(void) { return kSub; }
+extern "C" int moba_hip_decode_work_items(int Hq, int Hkv, int nslot) {
+  return (Hq / Hkv) * nslot;
+}
 
 extern "C" int moba_hip_paged_append(const void* k, const void* v, int dtype, int N, int Hkv, int D,
                                      void* k_cache, void* v_cache, int page_size,
@@ -509,22 +758,35 @@ extern "C" int moba_hip_block_means(const void* k_cache, int dtype, int Hkv, int
 extern "C" int moba_hip_decode_route(const void* q, int dtype, int Nq, int Hq, int Hkv, int D,
                                      const void* means, int max_chunks, const int* q_seq,
                                      const int* q_pos, int chunk, int width, int R, float* scores,
-                                     int* selected, void* stream) {
+                                     int* selected, void* work_items, int* work_counts,
+                                     void* stream) {
   if (R < 0 || R > kMaxRemote) { moba_set_error("decode_route: remote count must be in [0,8]"); return MOBA_ERR_ARG; }
   if (Hq % Hkv) { moba_set_error("decode_route: Hq must be a multiple of Hkv"); return MOBA_ERR_ARG; }
+  if (Hq / Hkv > 64) { moba_set_error("decode_route: at most 64 q heads per kv head"); return MOBA_ERR_ARG; }
   if (D < 1 || D > 256) { moba_set_error("decode_route: head_dim must be in [1,256]"); return MOBA_ERR_ARG; }
+  if (width < 0 || width > 8192) { moba_set_error("decode_route: width must be in [0,8192]"); return MOBA_ERR_ARG; }
   if (R > 0 && (scores == nullptr || width < 1)) { moba_set_error("decode_route: scores workspace [Nq,Hq,width] required"); return MOBA_ERR_ARG; }
-  const int64_t n = (int64_t)Nq * Hq;
-  if (n == 0) return MOBA_OK;
+  if (Nq <= 0) return MOBA_OK;
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == 0)
-    hipLaunchKernelGGL(route_kernel<0>, dim3((unsigned)n), dim3(64), 0, st, (const uint16_t*)q, Hq,
-                       Hkv, D, (const uint16_t*)means, max_chunks, q_seq, q_pos, chunk, width, R,
-                       scores, selected);
-  else
-    hipLaunchKernelGGL(route_kernel<1>, dim3((unsigned)n), dim3(64), 0, st, (const uint16_t*)q, Hq,
-                       Hkv, D, (const uint16_t*)means, max_chunks, q_seq, q_pos, chunk, width, R,
-                       scores, selected);
+  const int G = Hq / Hkv;
+  int nw = G < 16 ? G : 16;  // one wave per q head, bounded by the score buffers' LDS
+  const int wb = (width > 0 ? width : 1) * (int)sizeof(float);
+  while (nw > 1 && nw * wb > 96 * 1024) --nw;
+  const size_t lds = (size_t)nw * wb;
+  const int max_items = G * (R + 1);
+  dim3 grid((unsigned)(Nq * Hkv)), block(64 * nw);
+#define MOBA_ROUTE(DT_, DP_, VEC_)                                                              \
+  hipLaunchKernelGGL((route_kernel<DT_, DP_, VEC_>), grid, block, lds, st, (const uint16_t*)q,   \
+                     Hq, Hkv, D, (const uint16_t*)means, max_chunks, q_seq, q_pos, chunk, width, \
+                     R, scores, selected, (WorkItem*)work_items, work_counts, max_items)
+#define MOBA_ROUTE_D(DT_)                                                                       \
+  if (D % 8 != 0) MOBA_ROUTE(DT_, 8, false);                                                    \
+  else if (D <= 64) MOBA_ROUTE(DT_, 64, true);                                                  \
+  else if (D <= 128) MOBA_ROUTE(DT_, 128, true);                                                \
+  else MOBA_ROUTE(DT_, 256, true)
+  if (dtype == 0) { MOBA_ROUTE_D(0); } else { MOBA_ROUTE_D(1); }
+#undef MOBA_ROUTE_D
+#undef MOBA_ROUTE
   return moba_launch_status("decode_route");
 }
 
@@ -532,12 +794,16 @@ extern "C" int moba_hip_paged_attention(const void* q, int dtype, int Nq, int Hq
                                         const void* k_cache, const void* v_cache, int page_size,
                                         const int* table, int table_width, const int* lengths,
                                         const int* q_seq, const int* q_pos, const int* selected,
-                                        int nslot, int dense, int chunk, int max_chunks_bound,
-                                        float* part_o, float* part_ml, void* out, float* lse,
-                                        void* stream) {
+                                        int nslot, const void* work_items, const int* work_counts,
+                                        int dense, int chunk, int max_chunks_bound, float* part_o,
+                                        float* part_ml, void* out, float* lse, void* stream) {
   if (dtype != 0 && dtype != 1) { moba_set_error("paged_attention: dtype must be 0 or 1"); return MOBA_ERR_ARG; }
   if (D < 1 || D > 256) { moba_set_error("paged_attention: head_dim must be in [1,256]"); return MOBA_ERR_ARG; }
   if (Hq % Hkv) { moba_set_error("paged_attention: Hq must be a multiple of Hkv"); return MOBA_ERR_ARG; }
+  if (!dense && (nslot < 1 || nslot > 9 || work_items == nullptr || work_counts == nullptr)) {
+    moba_set_error("paged_attention: moba mode needs 1..9 slots and the route work list");
+    return MOBA_ERR_ARG;
+  }
   if (Nq <= 0) return MOBA_OK;
   AttnArgs a;
   a.q = (const uint16_t*)q; a.kc = (const uint16_t*)k_cache; a.vc = (const uint16_t*)v_cache;
@@ -545,12 +811,13 @@ extern "C" int moba_hip_paged_attention(const void* q, int dtype, int Nq, int Hq
   a.P = page_size; a.W = table_width; a.C = chunk;
   a.dense = dense ? 1 : 0;
   a.nslot = dense ? max_chunks_bound : nslot;
-  a.nsub = (chunk + kSub - 1) / kSub;
+  a.max_items = a.G * nslot;
   a.scale_log2 = (1.0f / sqrtf((float)D)) * kLog2e;
   a.table = table; a.lengths = lengths; a.seq = q_seq; a.pos = q_pos; a.selected = selected;
+  a.items = (const WorkItem*)work_items; a.item_counts = work_counts;
   a.part_o = part_o; a.part_ml = part_ml; a.out = (uint16_t*)out; a.lse = lse;
   const int n_items = dense ? max_chunks_bound : a.G * nslot;
-  if (n_items <= 0 || n_items > 65535 || a.nsub > 65535) { moba_set_error("paged_attention: work grid out of range"); return MOBA_ERR_ARG; }
+  if (n_items <= 0 || n_items > 65535) { moba_set_error("paged_attention: work grid out of range"); return MOBA_ERR_ARG; }
   hipStream_t st = (hipStream_t)stream;
   return dtype == 0 ? dispatch_attn<0>(a, n_items, st) : dispatch_attn<1>(a, n_items, st);
 }
@@ -562,4 +829,25 @@ extern "C" int moba_hip_decode_metadata(int* table, int table_width, int* length
   hipLaunchKernelGGL(metadata_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, table,
                      table_width, lengths, ids, positions, delta, B, append);
   return moba_launch_status("decode_metadata");
+}
+
+extern "C" int moba_hip_decode_step(int* table, int table_width, int* lengths, const int* ids,
+                                    int* positions, const int* delta, int B, const void* k,
+                                    const void* v, int dtype, void* k_cache, void* v_cache,
+                                    int page_size, int Hkv, int D, int chunk, void* means,
+                                    int max_chunks, void* stream) {
+  if (B <= 0) return MOBA_OK;
+  if (dtype != 0 && dtype != 1) { moba_set_error("decode_step: dtype must be 0 or 1"); return MOBA_ERR_ARG; }
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == 0)
+    hipLaunchKernelGGL(step_kernel<0>, dim3(B), dim3(256), 0, st, table, table_width, lengths, ids,
+                       positions, delta, B, (const uint16_t*)k, (const uint16_t*)v,
+                       (uint16_t*)k_cache, (uint16_t*)v_cache, page_size, Hkv, D, chunk,
+                       (uint16_t*)means, max_chunks);
+  else
+    hipLaunchKernelGGL(step_kernel<1>, dim3(B), dim3(256), 0, st, table, table_width, lengths, ids,
+                       positions, delta, B, (const uint16_t*)k, (const uint16_t*)v,
+                       (uint16_t*)k_cache, (uint16_t*)v_cache, page_size, Hkv, D, chunk,
+                       (uint16_t*)means, max_chunks);
+  return moba_launch_status("decode_step");
 }

@@ -231,12 +231,12 @@ class PagedKVCache:
         width = max(remote, max_history)
         if remote and width * hq * nq >= 2 ** 31:
             raise ValueError("route score grid exceeds int32 capacity")
-        selected = torch.empty((nq, hq, 1 + remote), dtype=torch.int32, device=self.device)
+        work = kernels.RouteWork(nq, hq, self.num_kv_heads, remote, self.device)
         scores = (torch.empty((nq, hq, width), dtype=torch.float32, device=self.device)
                   if remote else None)
         kernels.route(q, self._means, ids, positions, self.chunk_size, width if remote else 0,
-                      remote, scores, selected)
-        return selected
+                      remote, scores, work)
+        return work
 
     @torch.no_grad()
     def attend(self, q, *, sequence_ids, positions=None, topk=4, mode="moba"):
@@ -250,12 +250,12 @@ class PagedKVCache:
         q = q.contiguous()
         gpu_ids, gpu_pos = self._metadata(ids, pos) if gpu_metadata is None else gpu_metadata
         max_hist = max(pos) // self.chunk_size
-        selected = None if dense else self._route(q, gpu_ids, gpu_pos, topk, max_hist)
+        work = None if dense else self._route(q, gpu_ids, gpu_pos, topk, max_hist)
         out = torch.empty_like(q)
         lse = torch.empty(q.shape[:2], device=self.device, dtype=torch.float32)
         kernels.attention(q, self.k_cache, self.v_cache, self._table, self._lengths, gpu_ids,
-                          gpu_pos, selected, out, lse, self.chunk_size, dense, max_hist + 1)
-        return DecodeResult(out, lse, selected, ids, pos)
+                          gpu_pos, work, out, lse, self.chunk_size, dense, max_hist + 1)
+        return DecodeResult(out, lse, None if dense else work.selected, ids, pos)
 
     @torch.no_grad()
     def append_and_attend(self, q, k, v, *, sequence_ids, cu_seqlens=None, topk=4, mode="moba"):

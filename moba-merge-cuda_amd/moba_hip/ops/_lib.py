@@ -27,13 +27,16 @@ SIGNATURES = {
                              _P, _P, _P, _P, _I, _P, _P, _P, _P, _P],
     "moba_hip_prefill_bwd": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _I, _P, _I,
                              _P, _I, _P, _I, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P],
-    "moba_hip_decode_sub_tokens": [],
+    "moba_hip_decode_work_items": [_I, _I, _I],
     "moba_hip_paged_append": [_P, _P, _I, _I, _I, _I, _P, _P, _I, _P, _I, _P, _P, _P],
     "moba_hip_block_means": [_P, _I, _I, _I, _I, _P, _I, _P, _P, _I, _I, _I, _P, _I, _P],
-    "moba_hip_decode_route": [_P, _I, _I, _I, _I, _I, _P, _I, _P, _P, _I, _I, _I, _P, _P, _P],
+    "moba_hip_decode_route": [_P, _I, _I, _I, _I, _I, _P, _I, _P, _P, _I, _I, _I, _P, _P, _P,
+                              _P, _P],
     "moba_hip_paged_attention": [_P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _I, _P, _P, _P, _P, _I,
-                                 _I, _I, _I, _P, _P, _P, _P, _P],
+                                 _P, _P, _I, _I, _I, _P, _P, _P, _P, _P],
     "moba_hip_decode_metadata": [_P, _I, _P, _P, _P, _P, _I, _I, _P],
+    "moba_hip_decode_step": [_P, _I, _P, _P, _P, _P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P,
+                             _I, _P],
 }
 _RESTYPES = {"moba_hip_last_error": ctypes.c_char_p}
 

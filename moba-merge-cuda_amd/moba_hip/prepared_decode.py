@@ -7,8 +7,9 @@ overwritten by the next call).
 
 One step is a fixed launch sequence on the cache's stream, so it can be
 captured once as a graph (``torch.cuda.graph`` records HIP graphs on ROCm):
-    decode_metadata -> paged_append -> block_means(step mode) ->
-    decode_route (scores + stable top-k + slot list) -> paged_attention.
+    decode_step (page-table delta + positions + scatter + closing-chunk mean)
+    -> decode_route (scores + stable top-k + slot list + work list)
+    -> paged_attention (+ its slot combine).
 Host work per step is O(active batch) planning plus, only when a row starts a
 new page, one synchronous 2 x B int32 upload of the page-table delta.
 Every kernel of the sequence is from libmoba_hip.so; none issues a memset, so
@@ -62,9 +63,10 @@ class PreparedDecode:
             self.output = torch.empty_like(self.q)
             self.lse = torch.empty((b, h), device=dev, dtype=torch.float32)
             self.scores = torch.empty((b, h, width), device=dev, dtype=torch.float32)
-            self.selected = torch.empty((b, h, self.remote + 1), device=dev, dtype=torch.int32)
+            self._work = kernels.RouteWork(b, h, cache.num_kv_heads, self.remote, dev)
+            self.selected = self._work.selected
             nslot = self.max_chunks if self.dense else self.remote + 1
-            n = kernels.workspace_entries(b, h, nslot, C)
+            n = b * h * nslot
             self._part_o = torch.empty((n, d), device=dev, dtype=torch.float32)
             self._part_ml = torch.empty((n, 2), device=dev, dtype=torch.float32)
             self.gpu_ids = torch.tensor(self.ids, device=dev, dtype=torch.int32)
@@ -126,17 +128,17 @@ class PreparedDecode:
 
     def _compute(self, append):
         c = self.cache
-        kernels.metadata(c._table, c._lengths, self.gpu_ids, self.positions, self.delta, append)
-        if append:
-            kernels.append_tokens(self.k, self.v, c.k_cache, c.v_cache, c._table, self.gpu_ids,
-                                  self.positions)
-            kernels.block_means(c.k_cache, c._table, c._means, self.gpu_ids, self.positions,
-                                c.chunk_size, mode=1)
+        if append:  # metadata + scatter + closing-chunk mean in one launch
+            kernels.step(c._table, c._lengths, self.gpu_ids, self.positions, self.delta, self.k,
+                         self.v, c.k_cache, c.v_cache, c.chunk_size, c._means)
+        else:
+            kernels.metadata(c._table, c._lengths, self.gpu_ids, self.positions, self.delta,
+                             False)
         if not self.dense:
             kernels.route(self.q, c._means, self.gpu_ids, self.positions, c.chunk_size,
-                          self.scores.shape[-1], self.remote, self.scores, self.selected)
+                          self.scores.shape[-1], self.remote, self.scores, self._work)
         kernels.attention(self.q, c.k_cache, c.v_cache, c._table, c._lengths, self.gpu_ids,
-                          self.positions, self.selected, self.output, self.lse, c.chunk_size,
+                          self.positions, self._work, self.output, self.lse, c.chunk_size,
                           self.dense, self.max_chunks, self._part_o, self._part_ml)
 
     def _run(self, kind, use_graph):

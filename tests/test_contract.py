@@ -111,4 +111,7 @@ def test_argument_errors_are_reported_without_a_device():
                   None, None, None)
     with pytest.raises(_lib.MobaHipError, match="head_dim"):
         _lib.call("moba_hip_paged_attention", None, 0, 1, 1, 1, 300, None, None, 1, None, 1,
-                  None, None, None, None, 1, 0, 4, 1, None, None, None, None, None)
+                  None, None, None, None, 1, None, None, 0, 4, 1, None, None, None, None, None)
+    with pytest.raises(_lib.MobaHipError, match="work list"):
+        _lib.call("moba_hip_paged_attention", None, 0, 1, 1, 1, 64, None, None, 1, None, 1,
+                  None, None, None, None, 2, None, None, 0, 4, 1, None, None, None, None, None)
