@@ -26,6 +26,9 @@ FLAGS = [
     # packed fp32 ops are disabled on this pool (device-side flag; the host
     # pass warns that it does not know the feature).
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in VGPRs: no accumulator round trips through AGPRs for
+    # the short-lived S / dP tiles
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall", "-Wno-unused-result",
 ]
 

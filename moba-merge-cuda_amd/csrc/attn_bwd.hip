@@ -17,6 +17,8 @@
 //        rows of the chunk for all G heads of the group, then the expert rows
 //        that selected the chunk.  dK, dV accumulate in registers and are
 //        written once.
+#include <type_traits>
+
 #include "common.h"
 #include "../../include/moba_hip.h"
 
@@ -52,7 +54,6 @@ struct BwdArgs {
 };
 
 constexpr int kBN = 64;   // dq: keys per LDS tile
-constexpr int kBQ = 64;   // dkdv: query rows per LDS tile
 
 // ------------------------------------------------------------------ delta
 template <int DT>
@@ -283,166 +284,233 @@ __global__ __launch_bounds__(256, 1) void dq_kernel(BwdArgs a) {
 }
 
 // ------------------------------------------------------------------- dkdv
-// One workgroup owns 128 / DSPLIT keys of one chunk and one KV head; each
-// wave holds one 32-key block of K and V as MFMA B fragments.  Query tiles of
-// 64 rows (Q and dO, row-major) are double-buffered in LDS with the next tile
-// prefetched into registers.  S = Q K^T and dP = dO V^T leave one key per lane
-// (D-layout), which is exactly the A layout of P^T / dS^T for
-// dV += P^T dO and dK += dS^T Q; dO and Q enter as B through the transposed
-// LDS read.  DSPLIT waves share a key block and split its d range (DP = 256).
-template <int DT, int DP, int DSPLIT>
-__global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdArgs a) {
-  constexpr int QS = DP + 8, NKS = DP / 16, NDB = DP / 32 / DSPLIT;
-  constexpr int NLD = kBQ * DP / 8 / 256;
-  __shared__ __attribute__((aligned(16))) uint16_t Qs[2][kBQ * QS];
-  __shared__ __attribute__((aligned(16))) uint16_t Gs[2][kBQ * QS];
-  __shared__ __attribute__((aligned(16))) float lse2s[2][kBQ];
-  __shared__ __attribute__((aligned(16))) float dels[2][kBQ];
+// Key-major dK/dV.  A workgroup of 8 waves owns 128*KB keys of one chunk and
+// one KV head, as 4 pairs of waves; each pair owns 32*KB keys.  Within a pair
+// the work is split by role so that each wave holds only half the operands:
+//   role P (waves 0-3): K in registers; S = Q K^T, P = exp2(S*c - lse), P to
+//                       LDS (fp32), then dV += P^T dO
+//   role D (waves 4-7): V in registers; dP = dO V^T, reads P, dS = P (dP - delta),
+//                       then dK += dS^T Q
+// Query tiles of 32 rows (Q and dO, row-major) are double-buffered in LDS, the
+// next tile prefetched through registers.  The MFMA D-layout of S / dP (one
+// key per lane) is exactly the A layout of P^T / dS^T; dO and Q enter as B
+// through the transposed LDS read.  Each LDS fragment a wave reads feeds KB
+// key blocks.  Waves w and w+4 share a SIMD, so one wave's exponentials
+// overlap its partner's MFMAs.
+template <int DP> constexpr int dkdv_kb() { return DP == 128 ? 2 : 1; }
+
+template <int DT, int DP>
+__global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
+  constexpr int KB = dkdv_kb<DP>();
+  constexpr int QS = DP + 8, NKS = DP / 16, NDB = DP / 32;
+  constexpr int BQ = 32;                      // query rows per tile
+  constexpr int NLD = (BQ * DP / 8 + 511) / 512;
+  constexpr int WKEYS = 32 * KB;              // keys per wave pair
+  __shared__ __attribute__((aligned(16))) uint16_t Qs[2][BQ * QS];
+  __shared__ __attribute__((aligned(16))) uint16_t Gs[2][BQ * QS];
+  __shared__ __attribute__((aligned(16))) float lse2s[2][BQ];
+  __shared__ __attribute__((aligned(16))) float dels[2][BQ];
+  __shared__ float Ps[4][KB][16][64];         // P handed from role P to role D
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int qi = lane & 31, hh = lane >> 5;
-  const int kblk = wave / DSPLIT, dpart = wave % DSPLIT;
+  const int pair = wave & 3;
+  const bool role_p = wave < 4;
   const int D = a.D, G = a.G;
-  const int c = a.kv_tiles[3 * blockIdx.x], kt0 = a.kv_tiles[3 * blockIdx.x + 1];
-  const int f = a.kv_tiles[3 * blockIdx.x + 2];
-  const int kh = blockIdx.y;
+  const int4 tile = reinterpret_cast<const int4*>(a.kv_tiles)[blockIdx.x];
+  const int c = tile.x, kt0 = tile.y, f = tile.z, kh = tile.w;
+  if (c < 0) return;                        // padding entry of the XCD-ordered list
   const int c_lo = a.cu_chunk[c], c_hi = a.cu_chunk[c + 1];
   const int key0 = c_lo + kt0;              // first key of the workgroup
-  const int wkey0 = key0 + kblk * 32;       // first key of this wave
-  const int mykey = wkey0 + qi;             // this lane's key (B operand column)
-  const bool key_ok = mykey < c_hi;
+  const int wkey0 = key0 + pair * WKEYS;    // first key of this pair
 
-  u16x8_t kf[NKS], vf[NKS];
+  // The two roles run as separate instantiations of the body, so each wave's
+  // code holds only its own role's registers.
+  auto body = [&](auto role_tag) {
+    constexpr bool ROLE_P = decltype(role_tag)::value;
+    // role P holds K, role D holds V (B operands: column = key, k = d)
+    u16x8_t kv[KB][NKS];
+    const uint16_t* kvsrc = ROLE_P ? a.k : a.v;
 #pragma unroll
-  for (int ks = 0; ks < NKS; ++ks) {
-    const int d = ks * 16 + hh * 8;
-    const int64_t off = ((int64_t)mykey * a.Hkv + kh) * D + d;
-    kf[ks] = (key_ok && d < D) ? ld8(a.k + off) : zero8();
-    vf[ks] = (key_ok && d < D) ? ld8(a.v + off) : zero8();
-  }
-  f32x16_t dka[NDB], dva[NDB];
-#pragma unroll
-  for (int i = 0; i < NDB; ++i) { dka[i] = zero16(); dva[i] = zero16(); }
-
-  // query tiles: G * n_self causal tiles (rows from key0 to the chunk end, for
-  // every head of the group), then the expert's gathered rows
-  const int self_begin = key0;
-  const int n_self = (max(0, c_hi - self_begin) + kBQ - 1) / kBQ;
-  const int e = (f >= 0 && a.R > 0) ? f * a.Hkv + kh : -1;
-  const int n_rem = e >= 0 ? a.counts[e] : 0;
-  const int rbase = e >= 0 ? a.row_off[e] : 0;
-  const int n_tiles = G * n_self + (n_rem + kBQ - 1) / kBQ;
-
-  auto row_of = [&](int it, int qr) -> int {  // row index s*Hq+h, or -1
-    if (it < G * n_self) {
-      const int g = it / n_self, s = self_begin + (it % n_self) * kBQ + qr;
-      return s < c_hi ? s * a.Hq + kh * G + g : -1;
-    }
-    const int local = (it - G * n_self) * kBQ + qr;
-    return local < n_rem ? a.rows[rbase + local] / a.R : -1;
-  };
-
-  u16x8_t qr_[NLD], gr_[NLD];
-  float lse_r = INFINITY, del_r = 0.0f;
-  auto gload = [&](int it) {
-#pragma unroll
-    for (int i = 0; i < NLD; ++i) {
-      const int id = tid + i * 256, q = id / (DP / 8), dc = (id % (DP / 8)) * 8;
-      const int row = row_of(it, q);
-      const bool ok = row >= 0 && dc < D;
-      qr_[i] = ok ? ld8(a.q + (int64_t)row * D + dc) : zero8();
-      gr_[i] = ok ? ld8(a.dout + (int64_t)row * D + dc) : zero8();
-    }
-    if (tid < kBQ) {
-      const int row = row_of(it, tid);
-      lse_r = row >= 0 ? a.lse[row] * kLog2e : INFINITY;
-      del_r = row >= 0 ? a.delta[row] : 0.0f;
-    }
-  };
-  auto lstore = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < NLD; ++i) {
-      const int id = tid + i * 256, q = id / (DP / 8), dc = (id % (DP / 8)) * 8;
-      st8(&Qs[buf][q * QS + dc], qr_[i]);
-      st8(&Gs[buf][q * QS + dc], gr_[i]);
-    }
-    if (tid < kBQ) { lse2s[buf][tid] = lse_r; dels[buf][tid] = del_r; }
-  };
-
-  const float c2 = a.scale_log2;
-  if (n_tiles > 0) {
-    gload(0);
-    lstore(0);
-  }
-  __syncthreads();
-  for (int it = 0; it < n_tiles; ++it) {
-    const int buf = it & 1;
-    if (it + 1 < n_tiles) gload(it + 1);
-    const bool is_self = it < G * n_self;
-    const int sq0 = is_self ? self_begin + (it % n_self) * kBQ : 0;
-    const bool need_mask = (wkey0 + 32 > c_hi) || (is_self && sq0 < wkey0 + 31);
-
-    u16x8_t pv[2][2], dsv[2][2];
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      f32x16_t sa = zero16(), pa = zero16();
+    for (int kb = 0; kb < KB; ++kb) {
+      const int key = wkey0 + kb * 32 + qi;
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {
-        sa = mfma32<DT>(ld8(&Qs[buf][(qb * 32 + qi) * QS + ks * 16 + hh * 8]), kf[ks], sa);
-        pa = mfma32<DT>(ld8(&Gs[buf][(qb * 32 + qi) * QS + ks * 16 + hh * 8]), vf[ks], pa);
+        const int d = ks * 16 + hh * 8;
+        const bool ok = key < c_hi && d < D;
+        kv[kb][ks] = ok ? ld8(kvsrc + ((int64_t)key * a.Hkv + kh) * D + d) : zero8();
       }
-      float pt[16], dt[16];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int qb0 = qb * 32 + 8 * j + 4 * hh;
-        const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(&lse2s[buf][qb0]);
-        const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(&dels[buf][qb0]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = 4 * j + i;
-          float p = fast_exp2(fmaf(sa[r], c2, -l4[i]));
-          if (need_mask) p = (key_ok && (!is_self || mykey <= sq0 + qb0 + i)) ? p : 0.0f;
-          pt[r] = p;
-          dt[r] = p * (pa[r] - d4[i]);
-        }
-      }
-      pv[qb][0] = pack8<DT>(pt);
-      pv[qb][1] = pack8<DT>(pt + 8);
-      dsv[qb][0] = pack8<DT>(dt);
-      dsv[qb][1] = pack8<DT>(dt + 8);
     }
+    f32x16_t acc[KB][NDB];                    // dV (role P) or dK (role D)
 #pragma unroll
-    for (int i = 0; i < NDB; ++i) {
-      const int db = dpart * NDB + i;
+    for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const u16x8_t gt = ld_tr_operand(Gs[buf], QS, qb * 32 + t * 16, db * 32, lane);
-          const u16x8_t qt = ld_tr_operand(Qs[buf], QS, qb * 32 + t * 16, db * 32, lane);
-          dva[i] = mfma32<DT>(pv[qb][t], gt, dva[i]);
-          dka[i] = mfma32<DT>(dsv[qb][t], qt, dka[i]);
-        }
-    }
-    if (it + 1 < n_tiles) lstore(buf ^ 1);
-    __syncthreads();
-  }
+      for (int i = 0; i < NDB; ++i) acc[kb][i] = zero16();
 
-  // dK/dV D-layout: lane holds column d = db*32 + qi, keys 8j + 4hh + i.
-#pragma unroll
-  for (int i = 0; i < NDB; ++i) {
-    const int d = (dpart * NDB + i) * 32 + qi;
-    if (d >= D) continue;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = wkey0 + 8 * (r >> 2) + 4 * hh + (r & 3);
-      if (key < c_hi) {
-        const int64_t off = ((int64_t)key * a.Hkv + kh) * D + d;
-        a.dk[off] = from_f32<DT>(dka[i][r] * a.scale);
-        a.dv[off] = from_f32<DT>(dva[i][r]);
+    // query tiles: G * n_self causal tiles (rows from key0 to the chunk end, for
+    // every head of the group), then the expert's gathered rows
+    const int self_begin = key0;
+    const int n_self = (max(0, c_hi - self_begin) + BQ - 1) / BQ;
+    const int e = (f >= 0 && a.R > 0) ? f * a.Hkv + kh : -1;
+    const int n_rem = e >= 0 ? a.counts[e] : 0;
+    const int rbase = e >= 0 ? a.row_off[e] : 0;
+    const int n_tiles = G * n_self + (n_rem + BQ - 1) / BQ;
+
+    auto row_of = [&](int it, int qr) -> int {  // row index s*Hq+h, or -1
+      if (it < G * n_self) {
+        const int g = it / n_self, s = self_begin + (it % n_self) * BQ + qr;
+        return s < c_hi ? s * a.Hq + kh * G + g : -1;
       }
+      const int local = (it - G * n_self) * BQ + qr;
+      return local < n_rem ? a.rows[rbase + local] / a.R : -1;
+    };
+
+    // Row indices run one tile ahead of the Q/dO loads: a gathered expert row
+    // costs two dependent global loads (its index, then its data).
+    int nrow[NLD], nlrow = -1;
+    auto fetch_rows = [&](int it) {
+#pragma unroll
+      for (int i = 0; i < NLD; ++i) {
+        const int q = (tid + i * 512) / (DP / 8);
+        nrow[i] = q < BQ ? row_of(it, q) : -1;
+      }
+      nlrow = tid < BQ ? row_of(it, tid) : -1;
+    };
+    u16x8_t qr_[NLD], gr_[NLD];
+    float lse_r = INFINITY, del_r = 0.0f;
+    auto gload = [&]() {
+#pragma unroll
+      for (int i = 0; i < NLD; ++i) {
+        const int dc = ((tid + i * 512) % (DP / 8)) * 8;
+        const bool ok = nrow[i] >= 0 && dc < D;
+        qr_[i] = ok ? ld8(a.q + (int64_t)nrow[i] * D + dc) : zero8();
+        gr_[i] = ok ? ld8(a.dout + (int64_t)nrow[i] * D + dc) : zero8();
+      }
+      lse_r = nlrow >= 0 ? a.lse[nlrow] * kLog2e : INFINITY;
+      del_r = nlrow >= 0 ? a.delta[nlrow] : 0.0f;
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+      for (int i = 0; i < NLD; ++i) {
+        const int id = tid + i * 512, q = id / (DP / 8), dc = (id % (DP / 8)) * 8;
+        if (q < BQ) {
+          st8(&Qs[buf][q * QS + dc], qr_[i]);
+          st8(&Gs[buf][q * QS + dc], gr_[i]);
+        }
+      }
+      if (tid < BQ) { lse2s[buf][tid] = lse_r; dels[buf][tid] = del_r; }
+    };
+
+    const float c2 = a.scale_log2;
+    if (n_tiles > 0) {
+      fetch_rows(0);
+      gload();
+      lstore(0);
+      fetch_rows(1);
     }
-  }
+    __syncthreads();
+    for (int it = 0; it < n_tiles; ++it) {
+      const int buf = it & 1;
+      if (it + 1 < n_tiles) {
+        gload();
+        fetch_rows(it + 2);
+      }
+      const bool is_self = it < G * n_self;
+      const int sq0 = is_self ? self_begin + (it % n_self) * BQ : 0;
+      // causal rows that end before the pair's first key contribute nothing
+      const bool skip = is_self && sq0 + BQ - 1 < wkey0;
+      const bool need_mask = (wkey0 + WKEYS > c_hi) || (is_self && sq0 < wkey0 + WKEYS - 1);
+      // ---- first half: S -> P (role P) or dP (role D)
+      const uint16_t* A1 = ROLE_P ? Qs[buf] : Gs[buf];
+      f32x16_t sp[KB];
+      if (!skip) {
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) sp[kb] = zero16();
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+          const u16x8_t af = ld8(&A1[qi * QS + ks * 16 + hh * 8]);
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb) sp[kb] = mfma32<DT>(af, kv[kb][ks], sp[kb]);
+        }
+        if constexpr (ROLE_P) {
+          auto to_p = [&](auto mask_tag) {
+            constexpr bool MASK = decltype(mask_tag)::value;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int r0 = 8 * j + 4 * hh;
+              const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(&lse2s[buf][r0]);
+#pragma unroll
+              for (int kb = 0; kb < KB; ++kb) {
+                const int key = wkey0 + kb * 32 + qi;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                  float p = fast_exp2(fmaf(sp[kb][4 * j + i], c2, -l4[i]));
+                  if constexpr (MASK)
+                    p = (key < c_hi && (!is_self || key <= sq0 + r0 + i)) ? p : 0.0f;
+                  sp[kb][4 * j + i] = p;
+                  Ps[pair][kb][4 * j + i][lane] = p;
+                }
+              }
+            }
+          };
+          if (need_mask) to_p(std::true_type{}); else to_p(std::false_type{});
+        }
+      }
+      __syncthreads();
+      // ---- second half: dV += P^T dO (role P) or dK += dS^T Q (role D)
+      if (!skip) {
+        u16x8_t op[KB][2];
+        if constexpr (ROLE_P) {
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) op[kb][r >> 3][r & 7] = from_f32<DT>(sp[kb][r]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(&dels[buf][8 * j + 4 * hh]);
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                const int r = 4 * j + i;
+                const float p = Ps[pair][kb][r][lane];
+                op[kb][j >> 1][(j & 1) * 4 + i] = from_f32<DT>(p * (sp[kb][r] - d4[i]));
+              }
+          }
+        }
+        const uint16_t* B2 = ROLE_P ? Gs[buf] : Qs[buf];
+#pragma unroll
+        for (int i = 0; i < NDB; ++i) {
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            const u16x8_t bt = ld_tr_operand(B2, QS, t * 16, i * 32, lane);
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) acc[kb][i] = mfma32<DT>(op[kb][t], bt, acc[kb][i]);
+          }
+        }
+      }
+      if (it + 1 < n_tiles) lstore(buf ^ 1);
+      __syncthreads();
+    }
+
+    // D-layout: lane holds column d = i*32 + qi, keys 8j + 4hh + r.
+    uint16_t* dst = ROLE_P ? a.dv : a.dk;
+    const float osc = ROLE_P ? 1.0f : a.scale;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int i = 0; i < NDB; ++i) {
+        const int d = i * 32 + qi;
+        if (d >= D) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = wkey0 + kb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
+          if (key < c_hi) dst[((int64_t)key * a.Hkv + kh) * D + d] = from_f32<DT>(acc[kb][i][r] * osc);
+        }
+      }
+  };
+  if (role_p) body(std::true_type{}); else body(std::false_type{});
 }
 
 template <int DT, int DP>
@@ -457,10 +525,8 @@ int launch_bwd(const BwdArgs& a, int n_self, int n_kv, int max_remote, int parts
       hipLaunchKernelGGL((dq_kernel<DT, DP, false, DP <= 128 ? 2 : 1>), dim3(n_self, a.Hq), dim3(256), 0, st, a);
   }
   if ((parts & 2) && n_kv > 0) {
-    if constexpr (DP > 128)
-      hipLaunchKernelGGL((dkdv_kernel<DT, DP, 2>), dim3(n_kv, a.Hkv), dim3(256), 0, st, a);
-    else
-      hipLaunchKernelGGL((dkdv_kernel<DT, DP, 1>), dim3(n_kv, a.Hkv), dim3(256), 0, st, a);
+    // keys per workgroup: 4 wave pairs x 32*KB; the host's key tiles match
+    hipLaunchKernelGGL((dkdv_kernel<DT, DP>), dim3(n_kv), dim3(512), 0, st, a);
   }
   return moba_launch_status("prefill_bwd");
 }

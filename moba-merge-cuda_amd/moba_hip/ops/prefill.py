@@ -66,27 +66,56 @@ class PrefillPlan:
         self.max_remote_tiles = max_tiles
         self.chunk_start = [cu_chunk[c] for c in filtered]
         # key-major backward tiles: (chunk, first key, filtered index or -1)
-        self.kv_block = 64 if self.head_dim > 128 else 128
+        # keys per dkdv workgroup: 4 wave pairs x 32 x (2 for head dims 65..128, else 1)
+        self.kv_block = 256 if 64 < self.head_dim <= 128 else 128
         fidx = {c: i for i, c in enumerate(filtered)}
-        kv = []
-        for c in range(len(att_chunk) - 1):
-            length = att_chunk[c + 1] - att_chunk[c]
-            f = -1 if self.fallback else fidx.get(c, -1)
-            tail = 0 if f < 0 else cu[chunk_batch[c] + 1] - cu_chunk[c + 1]
-            kv.extend((tail, k0, c, f) for k0 in range(0, length, self.kv_block))
-        kv.sort(key=lambda x: (-x[0], x[1]))  # most expert rows first, then most causal rows
-        self.n_kv_tiles = len(kv)
-        kv_flat = [x for t in kv for x in t[2:3] + t[1:2] + t[3:4]]
+        self.kv_tiles_list = self._kv_tile_order(att_chunk, fidx, cu, chunk_batch, cu_chunk)
+        self.n_kv_tiles = len(self.kv_tiles_list) // 4
+        kv_flat = self.kv_tiles_list
 
         parts = OrderedDict(
             att_chunk=att_chunk, cu_chunk=cu_chunk, chunk_batch=chunk_batch, first_chunk=first,
             cu_seqlens=list(cu), filtered=filtered or [0], chunk_start=self.chunk_start or [0],
-            self_tiles=[x for t in tiles for x in t] or [0, 0], kv_tiles=kv_flat or [0, 0, -1])
+            self_tiles=[x for t in tiles for x in t] or [0, 0], kv_tiles=kv_flat or [-1, 0, -1, 0])
         flat, self._views = [], {}
         for name, vals in parts.items():
             self._views[name] = (len(flat), len(vals))
             flat.extend(vals)
         self.meta = torch.tensor(flat, dtype=torch.int32).to(device, non_blocking=False)
+
+    N_XCD = 8  # workgroup L of a 1-D grid runs on XCD L % 8
+
+    def _kv_tile_order(self, att_chunk, fidx, cu, chunk_batch, cu_chunk):
+        """dK/dV work list: (chunk, first key, filtered index or -1, kv head).
+
+        All key tiles of one (chunk, kv head) group go to one XCD, so the
+        query rows they share are fetched into that XCD's L2 once; groups are
+        dealt to XCDs in decreasing order of their query-row count.  Lists are
+        padded with empty tiles (chunk -1) to a common length and interleaved
+        so that entry L lands on XCD L % 8.
+        """
+        groups = []
+        for c in range(len(att_chunk) - 1):
+            length = att_chunk[c + 1] - att_chunk[c]
+            f = -1 if self.fallback else fidx.get(c, -1)
+            tail = 0 if f < 0 else cu[chunk_batch[c] + 1] - cu_chunk[c + 1]
+            cost = self.groups * (length + tail * self.remote / max(1, self.num_filtered))
+            tiles = list(range(0, length, self.kv_block))
+            for kh in range(self.hkv):
+                groups.append((cost, c, f, kh, tiles))
+        groups.sort(key=lambda g: (-g[0], g[1], g[3]))
+        per = [[] for _ in range(self.N_XCD)]
+        load = [0.0] * self.N_XCD
+        for cost, c, f, kh, tiles in groups:
+            x = min(range(self.N_XCD), key=lambda i: (load[i], i))
+            load[x] += cost
+            per[x].extend((c, k0, f, kh) for k0 in tiles)
+        n = max(len(p) for p in per) if per else 0
+        out = []
+        for i in range(n):
+            for x in range(self.N_XCD):
+                out.extend(per[x][i] if i < len(per[x]) else (-1, 0, -1, 0))
+        return out
 
     def dev(self, name):
         off, n = self._views[name]
