@@ -92,8 +92,8 @@ int moba_hip_prefill_fwd(const void* q, const void* k, const void* v, int dtype,
  * both _flash_attn_varlen_backward calls plus the autograd scatter of the
  * packed remote grads (grouped_attention.py:81-89).  out/dout [T,Hq,D],
  * lse [T,Hq] from the forward; kv_tiles[n_kv_tiles][4] = (chunk, first key,
- * filtered index or -1, kv head): one workgroup per entry, tiles of 256 keys
- * when 64 < D <= 128, else 128 keys; chunk -1 marks an empty entry.  delta [T*Hq] and
+ * filtered index or -1, kv head): one workgroup per entry, tiles of 128
+ * keys; chunk -1 marks an empty entry.  delta [T*Hq] and
  * part_dq [T*Hq*R, D] fp32 are workspaces.  dq [T,Hq,D], dk/dv [T,Hkv,D]
  * (dtype) are fully written (every key belongs to exactly one kv tile).
  * parts selects the launches: 1 = Delta and dq (query-major kernels), 2 = dk/dv

@@ -94,8 +94,8 @@ __global__ __launch_bounds__(256, 1) void dq_kernel(BwdArgs a) {
   bool valid[QB];
   int kh, k_lo, k_hi, s_wave0 = 0;
   if constexpr (REMOTE) {
-    const int t = blockIdx.x;
-    if (t >= a.tile_off[a.E]) return;
+    const int t = xcd_contiguous(blockIdx.x, a.tile_off[a.E]);
+    if (t < 0) return;
     int lo = 0, hi = a.E - 1;
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
@@ -284,68 +284,66 @@ __global__ __launch_bounds__(256, 1) void dq_kernel(BwdArgs a) {
 }
 
 // ------------------------------------------------------------------- dkdv
-// Key-major dK/dV.  A workgroup of 8 waves owns 128*KB keys of one chunk and
-// one KV head, as 4 pairs of waves; each pair owns 32*KB keys.  Within a pair
-// the work is split by role so that each wave holds only half the operands:
+// Key-major dK/dV.  A workgroup of 8 waves owns 128 keys of one chunk and one
+// KV head, as 4 pairs of waves; each pair owns 32 keys.  Within a pair the
+// work is split by role so that each wave holds only half the operands:
 //   role P (waves 0-3): K in registers; S = Q K^T, P = exp2(S*c - lse), P to
 //                       LDS (fp32), then dV += P^T dO
 //   role D (waves 4-7): V in registers; dP = dO V^T, reads P, dS = P (dP - delta),
 //                       then dK += dS^T Q
-// Query tiles of 32 rows (Q and dO, row-major) are double-buffered in LDS, the
-// next tile prefetched through registers.  The MFMA D-layout of S / dP (one
-// key per lane) is exactly the A layout of P^T / dS^T; dO and Q enter as B
-// through the transposed LDS read.  Each LDS fragment a wave reads feeds KB
-// key blocks.  Waves w and w+4 share a SIMD, so one wave's exponentials
-// overlap its partner's MFMAs.
-template <int DP> constexpr int dkdv_kb() { return DP == 128 ? 2 : 1; }
+// Query tiles of 32*QB rows (Q and dO, row-major) are double-buffered in LDS,
+// the next tile prefetched through registers and its row indices one tile
+// further ahead (a gathered expert row costs two dependent global loads: its
+// index, then its data).  The MFMA D-layout of S / dP (one key per lane) is
+// exactly the A layout of P^T / dS^T; dO and Q enter as B through the
+// transposed LDS read.  Waves w and w+4 share a SIMD, so one wave's
+// exponentials overlap its partner's MFMAs.
+constexpr int kDkdvPairKeys = 32;
+
+template <int DP> constexpr int dkdv_qb() { return DP <= 128 ? 2 : 1; }
 
 template <int DT, int DP>
 __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
-  constexpr int KB = dkdv_kb<DP>();
+  constexpr int QB = dkdv_qb<DP>();
   constexpr int QS = DP + 8, NKS = DP / 16, NDB = DP / 32;
-  constexpr int BQ = 32;                      // query rows per tile
+  constexpr int BQ = 32 * QB;                 // query rows per tile
   constexpr int NLD = (BQ * DP / 8 + 511) / 512;
-  constexpr int WKEYS = 32 * KB;              // keys per wave pair
+  constexpr int WKEYS = kDkdvPairKeys;        // keys per wave pair
   __shared__ __attribute__((aligned(16))) uint16_t Qs[2][BQ * QS];
   __shared__ __attribute__((aligned(16))) uint16_t Gs[2][BQ * QS];
   __shared__ __attribute__((aligned(16))) float lse2s[2][BQ];
   __shared__ __attribute__((aligned(16))) float dels[2][BQ];
-  __shared__ float Ps[4][KB][16][64];         // P handed from role P to role D
+  __shared__ float Ps[4][QB][16][64];         // P handed from role P to role D
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int qi = lane & 31, hh = lane >> 5;
   const int pair = wave & 3;
   const bool role_p = wave < 4;
   const int D = a.D, G = a.G;
-  const int4 tile = reinterpret_cast<const int4*>(a.kv_tiles)[blockIdx.x];
-  const int c = tile.x, kt0 = tile.y, f = tile.z, kh = tile.w;
+  const int* tile = a.kv_tiles + 4 * blockIdx.x;
+  const int c = tile[0], kt0 = tile[1], f = tile[2], kh = tile[3];
   if (c < 0) return;                        // padding entry of the XCD-ordered list
   const int c_lo = a.cu_chunk[c], c_hi = a.cu_chunk[c + 1];
   const int key0 = c_lo + kt0;              // first key of the workgroup
   const int wkey0 = key0 + pair * WKEYS;    // first key of this pair
+  const int mykey = wkey0 + qi;             // this lane's key (B operand column)
 
   // The two roles run as separate instantiations of the body, so each wave's
   // code holds only its own role's registers.
   auto body = [&](auto role_tag) {
     constexpr bool ROLE_P = decltype(role_tag)::value;
     // role P holds K, role D holds V (B operands: column = key, k = d)
-    u16x8_t kv[KB][NKS];
+    u16x8_t kv[NKS];
     const uint16_t* kvsrc = ROLE_P ? a.k : a.v;
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) {
-      const int key = wkey0 + kb * 32 + qi;
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) {
-        const int d = ks * 16 + hh * 8;
-        const bool ok = key < c_hi && d < D;
-        kv[kb][ks] = ok ? ld8(kvsrc + ((int64_t)key * a.Hkv + kh) * D + d) : zero8();
-      }
+    for (int ks = 0; ks < NKS; ++ks) {
+      const int d = ks * 16 + hh * 8;
+      const bool ok = mykey < c_hi && d < D;
+      kv[ks] = ok ? ld8(kvsrc + ((int64_t)mykey * a.Hkv + kh) * D + d) : zero8();
     }
-    f32x16_t acc[KB][NDB];                    // dV (role P) or dK (role D)
+    f32x16_t acc[NDB];                        // dV (role P) or dK (role D)
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-      for (int i = 0; i < NDB; ++i) acc[kb][i] = zero16();
+    for (int i = 0; i < NDB; ++i) acc[i] = zero16();
 
     // query tiles: G * n_self causal tiles (rows from key0 to the chunk end, for
     // every head of the group), then the expert's gathered rows
@@ -365,8 +363,6 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
       return local < n_rem ? a.rows[rbase + local] / a.R : -1;
     };
 
-    // Row indices run one tile ahead of the Q/dO loads: a gathered expert row
-    // costs two dependent global loads (its index, then its data).
     int nrow[NLD], nlrow = -1;
     auto fetch_rows = [&](int it) {
 #pragma unroll
@@ -422,36 +418,33 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
       const bool need_mask = (wkey0 + WKEYS > c_hi) || (is_self && sq0 < wkey0 + WKEYS - 1);
       // ---- first half: S -> P (role P) or dP (role D)
       const uint16_t* A1 = ROLE_P ? Qs[buf] : Gs[buf];
-      f32x16_t sp[KB];
+      f32x16_t sp[QB];
       if (!skip) {
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) sp[kb] = zero16();
+        for (int qb = 0; qb < QB; ++qb) sp[qb] = zero16();
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-          const u16x8_t af = ld8(&A1[qi * QS + ks * 16 + hh * 8]);
+        for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
-          for (int kb = 0; kb < KB; ++kb) sp[kb] = mfma32<DT>(af, kv[kb][ks], sp[kb]);
-        }
+          for (int qb = 0; qb < QB; ++qb)
+            sp[qb] = mfma32<DT>(ld8(&A1[(qb * 32 + qi) * QS + ks * 16 + hh * 8]), kv[ks], sp[qb]);
         if constexpr (ROLE_P) {
           auto to_p = [&](auto mask_tag) {
             constexpr bool MASK = decltype(mask_tag)::value;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const int r0 = 8 * j + 4 * hh;
-              const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(&lse2s[buf][r0]);
+            for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
-              for (int kb = 0; kb < KB; ++kb) {
-                const int key = wkey0 + kb * 32 + qi;
+              for (int j = 0; j < 4; ++j) {
+                const int r0 = qb * 32 + 8 * j + 4 * hh;
+                const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(&lse2s[buf][r0]);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                  float p = fast_exp2(fmaf(sp[kb][4 * j + i], c2, -l4[i]));
+                  float p = fast_exp2(fmaf(sp[qb][4 * j + i], c2, -l4[i]));
                   if constexpr (MASK)
-                    p = (key < c_hi && (!is_self || key <= sq0 + r0 + i)) ? p : 0.0f;
-                  sp[kb][4 * j + i] = p;
-                  Ps[pair][kb][4 * j + i][lane] = p;
+                    p = (mykey < c_hi && (!is_self || mykey <= sq0 + r0 + i)) ? p : 0.0f;
+                  sp[qb][4 * j + i] = p;
+                  Ps[pair][qb][4 * j + i][lane] = p;
                 }
               }
-            }
           };
           if (need_mask) to_p(std::true_type{}); else to_p(std::false_type{});
         }
@@ -459,36 +452,36 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
       __syncthreads();
       // ---- second half: dV += P^T dO (role P) or dK += dS^T Q (role D)
       if (!skip) {
-        u16x8_t op[KB][2];
+        u16x8_t op[QB][2];
         if constexpr (ROLE_P) {
 #pragma unroll
-          for (int kb = 0; kb < KB; ++kb)
+          for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) op[kb][r >> 3][r & 7] = from_f32<DT>(sp[kb][r]);
+            for (int r = 0; r < 16; ++r) op[qb][r >> 3][r & 7] = from_f32<DT>(sp[qb][r]);
         } else {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(&dels[buf][8 * j + 4 * hh]);
+          for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
-            for (int kb = 0; kb < KB; ++kb)
+            for (int j = 0; j < 4; ++j) {
+              const f32x4_t d4 =
+                  *reinterpret_cast<const f32x4_t*>(&dels[buf][qb * 32 + 8 * j + 4 * hh]);
 #pragma unroll
               for (int i = 0; i < 4; ++i) {
                 const int r = 4 * j + i;
-                const float p = Ps[pair][kb][r][lane];
-                op[kb][j >> 1][(j & 1) * 4 + i] = from_f32<DT>(p * (sp[kb][r] - d4[i]));
+                const float p = Ps[pair][qb][r][lane];
+                op[qb][j >> 1][(j & 1) * 4 + i] = from_f32<DT>(p * (sp[qb][r] - d4[i]));
               }
-          }
+            }
         }
         const uint16_t* B2 = ROLE_P ? Gs[buf] : Qs[buf];
 #pragma unroll
-        for (int i = 0; i < NDB; ++i) {
+        for (int i = 0; i < NDB; ++i)
 #pragma unroll
-          for (int t = 0; t < 2; ++t) {
-            const u16x8_t bt = ld_tr_operand(B2, QS, t * 16, i * 32, lane);
+          for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
-            for (int kb = 0; kb < KB; ++kb) acc[kb][i] = mfma32<DT>(op[kb][t], bt, acc[kb][i]);
-          }
-        }
+            for (int t = 0; t < 2; ++t)
+              acc[i] = mfma32<DT>(op[qb][t], ld_tr_operand(B2, QS, qb * 32 + t * 16, i * 32, lane),
+                                  acc[i]);
       }
       if (it + 1 < n_tiles) lstore(buf ^ 1);
       __syncthreads();
@@ -498,17 +491,15 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
     uint16_t* dst = ROLE_P ? a.dv : a.dk;
     const float osc = ROLE_P ? 1.0f : a.scale;
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb)
+    for (int i = 0; i < NDB; ++i) {
+      const int d = i * 32 + qi;
+      if (d >= D) continue;
 #pragma unroll
-      for (int i = 0; i < NDB; ++i) {
-        const int d = i * 32 + qi;
-        if (d >= D) continue;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = wkey0 + kb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
-          if (key < c_hi) dst[((int64_t)key * a.Hkv + kh) * D + d] = from_f32<DT>(acc[kb][i][r] * osc);
-        }
+      for (int r = 0; r < 16; ++r) {
+        const int key = wkey0 + 8 * (r >> 2) + 4 * hh + (r & 3);
+        if (key < c_hi) dst[((int64_t)key * a.Hkv + kh) * D + d] = from_f32<DT>(acc[i][r] * osc);
       }
+    }
   };
   if (role_p) body(std::true_type{}); else body(std::false_type{});
 }
@@ -520,12 +511,12 @@ int launch_bwd(const BwdArgs& a, int n_self, int n_kv, int max_remote, int parts
     hipLaunchKernelGGL(delta_kernel<DT>, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, st,
                        a.out, a.dout, rows, a.D, a.delta);
     if (max_remote > 0 && a.R > 0)
-      hipLaunchKernelGGL((dq_kernel<DT, DP, true, DP <= 128 ? 2 : 1>), dim3(max_remote), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((dq_kernel<DT, DP, true, DP <= 128 ? 2 : 1>), dim3((max_remote + 7) / 8 * 8), dim3(256), 0, st, a);
     if (n_self > 0)
       hipLaunchKernelGGL((dq_kernel<DT, DP, false, DP <= 128 ? 2 : 1>), dim3(n_self, a.Hq), dim3(256), 0, st, a);
   }
   if ((parts & 2) && n_kv > 0) {
-    // keys per workgroup: 4 wave pairs x 32*KB; the host's key tiles match
+    // 4 wave pairs x kDkdvPairKeys keys per workgroup; the host's key tiles match
     hipLaunchKernelGGL((dkdv_kernel<DT, DP>), dim3(n_kv), dim3(512), 0, st, a);
   }
   return moba_launch_status("prefill_bwd");

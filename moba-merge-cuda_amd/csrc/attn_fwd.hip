@@ -76,8 +76,8 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(FwdArgs a) {
   bool valid[QB];
   int kh, k_lo, k_hi, s_wave0 = 0;
   if constexpr (REMOTE) {
-    const int t = blockIdx.x;
-    if (t >= a.tile_off[a.E]) return;
+    const int t = xcd_contiguous(blockIdx.x, a.tile_off[a.E]);
+    if (t < 0) return;
     int lo = 0, hi = a.E - 1;
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
@@ -318,7 +318,7 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(FwdArgs a) {
 template <int DT, int DP>
 int launch_fwd(const FwdArgs& a, int n_self_tiles, int max_remote_tiles, hipStream_t st) {
   if (max_remote_tiles > 0 && a.R > 0) {
-    hipLaunchKernelGGL((fwd_kernel<DT, DP, true, DP <= 128 ? 2 : 1>), dim3(max_remote_tiles), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((fwd_kernel<DT, DP, true, DP <= 128 ? 2 : 1>), dim3((max_remote_tiles + 7) / 8 * 8), dim3(256), 0, st, a);
     int rc = moba_launch_status("prefill_fwd(remote)");
     if (rc) return rc;
   }

@@ -113,6 +113,17 @@ MOBA_DEV u16x8_t ld_tr_operand(const uint16_t* X, int ld, int g16, int c0, int l
   return r;
 }
 
+// Workgroup L of a 1-D grid runs on XCD L % 8 (8 XCDs, each with its own L2).
+// Maps L to a work index so that every XCD takes one contiguous eighth of
+// [0, total) in order: neighbouring work items, which share K/V tiles, stay in
+// one L2.  The grid must hold at least 8 * ceil(total / 8) workgroups; surplus
+// workgroups get -1.
+MOBA_DEV int xcd_contiguous(int L, int total) {
+  const int per = (total + 7) >> 3;
+  const int i = L >> 3, t = (L & 7) * per + i;
+  return (i < per && t < total) ? t : -1;
+}
+
 MOBA_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 template <int DT> MOBA_DEV u16x8_t pack8(const float* v) {

@@ -17,6 +17,11 @@ from . import _lib
 DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1}
 
 
+def dkdv_keys(head_dim):
+    """Keys per dK/dV workgroup: 4 wave pairs x 32 keys."""
+    return 128
+
+
 class PrefillPlan:
     """Chunk metadata + tile lists for one (cu_seqlens, chunk, Hq, Hkv) shape."""
 
@@ -66,8 +71,7 @@ class PrefillPlan:
         self.max_remote_tiles = max_tiles
         self.chunk_start = [cu_chunk[c] for c in filtered]
         # key-major backward tiles: (chunk, first key, filtered index or -1)
-        # keys per dkdv workgroup: 4 wave pairs x 32 x (2 for head dims 65..128, else 1)
-        self.kv_block = 256 if 64 < self.head_dim <= 128 else 128
+        self.kv_block = dkdv_keys(head_dim)
         fidx = {c: i for i, c in enumerate(filtered)}
         self.kv_tiles_list = self._kv_tile_order(att_chunk, fidx, cu, chunk_batch, cu_chunk)
         self.n_kv_tiles = len(self.kv_tiles_list) // 4
