@@ -80,7 +80,7 @@ __global__ __launch_bounds__(256) void delta_kernel(const uint16_t* __restrict__
 // in LDS (row-major).  S^T = K Q^T and dP^T = V dO^T take K / V rows as the A
 // operand; dQ^T = K^T dS^T reads K^T with the transposed LDS read.
 template <int DT, int DP, bool REMOTE, int QB>
-__global__ __launch_bounds__(256, 1) void dq_kernel(BwdArgs a) {
+__global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a) {
   constexpr int KS = DP + 8, NKS = DP / 16, NDB = DP / 32;
   constexpr int NLD = kBN * DP / 8 / 256;
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kBN * KS];
@@ -511,9 +511,9 @@ int launch_bwd(const BwdArgs& a, int n_self, int n_kv, int max_remote, int parts
     hipLaunchKernelGGL(delta_kernel<DT>, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, st,
                        a.out, a.dout, rows, a.D, a.delta);
     if (max_remote > 0 && a.R > 0)
-      hipLaunchKernelGGL((dq_kernel<DT, DP, true, DP <= 128 ? 2 : 1>), dim3((max_remote + 7) / 8 * 8), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((dq_kernel<DT, DP, true, attn_qb<DP>()>), dim3((max_remote + 7) / 8 * 8), dim3(256), 0, st, a);
     if (n_self > 0)
-      hipLaunchKernelGGL((dq_kernel<DT, DP, false, DP <= 128 ? 2 : 1>), dim3(n_self, a.Hq), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((dq_kernel<DT, DP, false, attn_qb<DP>()>), dim3(n_self, a.Hq), dim3(256), 0, st, a);
   }
   if ((parts & 2) && n_kv > 0) {
     // 4 wave pairs x kDkdvPairKeys keys per workgroup; the host's key tiles match

@@ -60,7 +60,7 @@ constexpr int kBN = 64;   // keys per LDS tile
 constexpr float kRescaleSlack = 8.0f;  // log2 headroom before O is rescaled
 
 template <int DT, int DP, bool REMOTE, int QB>
-__global__ __launch_bounds__(256, 1) void fwd_kernel(FwdArgs a) {
+__global__ __launch_bounds__(256, attn_occupancy<DP>()) void fwd_kernel(FwdArgs a) {
   constexpr int KS = DP + 8;    // row stride (elements) of the K and V tiles
   constexpr int NKS = DP / 16;  // k-steps of the QK^T contraction
   constexpr int NDB = DP / 32;  // 32-row d blocks of O^T
@@ -318,12 +318,12 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(FwdArgs a) {
 template <int DT, int DP>
 int launch_fwd(const FwdArgs& a, int n_self_tiles, int max_remote_tiles, hipStream_t st) {
   if (max_remote_tiles > 0 && a.R > 0) {
-    hipLaunchKernelGGL((fwd_kernel<DT, DP, true, DP <= 128 ? 2 : 1>), dim3((max_remote_tiles + 7) / 8 * 8), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((fwd_kernel<DT, DP, true, attn_qb<DP>()>), dim3((max_remote_tiles + 7) / 8 * 8), dim3(256), 0, st, a);
     int rc = moba_launch_status("prefill_fwd(remote)");
     if (rc) return rc;
   }
   if (n_self_tiles > 0) {
-    hipLaunchKernelGGL((fwd_kernel<DT, DP, false, DP <= 128 ? 2 : 1>), dim3(n_self_tiles, a.Hq), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((fwd_kernel<DT, DP, false, attn_qb<DP>()>), dim3(n_self_tiles, a.Hq), dim3(256), 0, st, a);
     return moba_launch_status("prefill_fwd(self)");
   }
   return MOBA_OK;

@@ -113,6 +113,12 @@ MOBA_DEV u16x8_t ld_tr_operand(const uint16_t* X, int ld, int g16, int c0, int l
   return r;
 }
 
+// 32-row query blocks per wave in the query-major attention kernels (forward
+// and dQ); a workgroup of 4 waves covers 128 * attn_qb rows.  One block per
+// wave leaves room for two waves per SIMD.
+template <int DP> constexpr int attn_qb() { return 1; }
+template <int DP> constexpr int attn_occupancy() { return attn_qb<DP>() == 1 ? 2 : 1; }
+
 // Workgroup L of a 1-D grid runs on XCD L % 8 (8 XCDs, each with its own L2).
 // Maps L to a work index so that every XCD takes one contiguous eighth of
 // [0, total) in order: neighbouring work items, which share K/V tiles, stay in

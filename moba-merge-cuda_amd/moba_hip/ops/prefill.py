@@ -17,6 +17,11 @@ from . import _lib
 DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1}
 
 
+def attn_rows(head_dim):
+    """Query rows per forward / dQ workgroup: 4 waves x 32 rows."""
+    return 128
+
+
 def dkdv_keys(head_dim):
     """Keys per dK/dV workgroup: 4 wave pairs x 32 keys."""
     return 128
@@ -31,8 +36,7 @@ class PrefillPlan:
         self.chunk = chunk
         self.hq, self.hkv = hq, hkv
         self.groups = hq // hkv
-        # query rows per attention workgroup: 4 waves x (2 or 1) blocks x 32
-        self.block_rows = 256 if head_dim <= 128 else 128
+        self.block_rows = attn_rows(head_dim)
         BLOCK_ROWS = self.block_rows
         cu_chunk, chunk_batch, filtered = [0], [], []
         for b in range(len(cu) - 1):
