@@ -7,7 +7,9 @@ Default run (N=1):
                 Q/K/V/dO iid N(0,1)/sqrt(128)); ms per step and MFMA%
                 (algorithmic FLOPs: attended pairs x (4D fwd + 10D bwd)).
   * roofline  : the key-major dK/dV backward kernel, timed live with stream
-                events around its launch inside every timed step.
+                events around its launch inside every timed step; `traffic`
+                is its HBM bytes per launch from the copy-calibrated rocprofv3
+                FETCH_SIZE / WRITE_SIZE passes in profiles/dkdv_cfg3_traffic.*.
   * gqa_16k   : cfg2 (Qwen2-0.5B GQA 14/2, D=64, T=16384, chunk 2048).
   * decode    : cfg4, batch-8 paged decode (12q/2kv, D=128, bf16, ctx
                 U[2048,16384], page 48, chunk 512, topk 4, shuffled page pool),
@@ -250,6 +252,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--only", choices=["prefill", "decode"], default=None)
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="first run one 1 GiB device-to-device copy (a known-size kernel that "
+                         "calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one MI355X: multi-GPU runs are not part of this build "
@@ -259,6 +264,13 @@ def main():
     import torch
     torch.cuda.set_device(0)
 
+    if args.calib_copy:
+        src = torch.ones(1 << 29, dtype=torch.int16, device="cuda")  # 1 GiB
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        torch.cuda.empty_cache()
     out = {"metric": METRIC}
     res3 = None
     if args.only in (None, "prefill"):
@@ -282,6 +294,10 @@ def main():
 
     if res3 is not None:
         ach = res3["dkdv_tflop"] / (res3["dkdv_ms"] * 1e-3)
+        traffic = None
+        tfile = ROOT / "profiles" / "dkdv_cfg3_traffic.json"
+        if tfile.exists():  # rocprofv3 FETCH_SIZE + WRITE_SIZE passes, copy-calibrated
+            traffic = json.loads(tfile.read_text())["traffic_bytes"]
         out.update({
             "value": round(res3["ms_per_step"], 3), "unit": "ms per 32K MHA prefill fwd+bwd step",
             "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -295,7 +311,8 @@ def main():
             "tflops": round(res3["tflops"], 1),
             "roofline": {"bound": "mfma", "kernel": "dkdv_kernel<bf16,128>",
                          "achieved": round(ach, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(ach / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                         "frac": round(ach / BF16_PEAK_TFLOPS, 4), "traffic": traffic,
+                         "traffic_unit": "bytes per launch (profiles/dkdv_cfg3_traffic.md)",
                          "avg_launch_ms": round(res3["dkdv_ms"], 3),
                          "algorithmic_tflop_per_launch": round(res3["dkdv_tflop"], 3)},
             "prefill_32k": res3, "gqa_16k": res2,
