@@ -163,7 +163,7 @@ def bench_decode(batch, hq, hkv, d, page, chunk, topk, lo, hi, steps, warmup, dt
     elem = 2
     rng = random.Random(seed)
     lengths = [rng.randint(lo, hi) for _ in range(batch)]
-    extra = warmup + steps + 4
+    extra = 2 * (warmup + steps) + 4
     g = torch.Generator(device="cuda").manual_seed(seed + 1)
     q = torch.randn((batch, hq, d), generator=g, device="cuda", dtype=dtype)
     kn = torch.randn((batch, hkv, d), generator=g, device="cuda", dtype=dtype)
@@ -181,39 +181,47 @@ def bench_decode(batch, hq, hkv, d, page, chunk, topk, lo, hi, steps, warmup, dt
     del cache
     torch.cuda.empty_cache()
 
-    # pass 2 (timed): identical state, graph replay
+    # pass 2 (timed): identical state; eager steps, then graph-replayed steps
     cache = build_cache(batch, lengths, hq, hkv, d, page, chunk, dtype, extra, seed)
-    with cache.prepare_decode(list(range(batch)), hq, topk=topk, check_finite=False) as p:
-        p.capture("step")
-        for _ in range(warmup):
-            p.step(q, kn, vn, use_graph=True)
+
+    def timed(fn, n):
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
         e0.record()
-        for _ in range(steps):
-            p.step(q, kn, vn, use_graph=True)
+        for _ in range(n):
+            fn()
         e1.record()
         torch.cuda.synchronize()
-        wall_us = (time.perf_counter() - t0) * 1e6 / steps
-        gpu_us = e0.elapsed_time(e1) * 1e3 / steps
-        # kernel-only time of an attend graph (reads the cache, mutates nothing:
-        # replaying the step graph without host page planning would append
-        # past the pages the allocator handed out)
-        p.capture("attend")
-        e2, e3 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e2.record()
-        for _ in range(20):
-            p._graphs["attend"].replay()
-        e3.record()
-        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e6 / n, e0.elapsed_time(e1) * 1e3 / n
+
+    with cache.prepare_decode(list(range(batch)), hq, topk=topk, check_finite=False) as p:
+        # the prepared workspaces are the inputs (no staging copies)
+        p.q.copy_(q)
+        p.k.copy_(kn)
+        p.v.copy_(vn)
+        for _ in range(warmup):
+            p.step(p.q, p.k, p.v)
+        eager_wall, eager_gpu = timed(lambda: p.step(p.q, p.k, p.v), steps)
+        p.capture("step")
+        for _ in range(warmup):
+            p.step(p.q, p.k, p.v, use_graph=True)
+        graph_wall, graph_gpu = timed(lambda: p.step(p.q, p.k, p.v, use_graph=True), steps)
+        # device time of the decode work alone: back-to-back attend launches
+        # (they read the cache and mutate nothing)
+        _, kernel_us = timed(lambda: p._compute(False), 50)
+        fused = p._fused is not None
     del cache
     torch.cuda.empty_cache()
     mean_bytes = float(np.mean(byte_counts))
-    return {"us_per_step": wall_us, "gpu_us_per_step": gpu_us,
-            "attend_graph_replay_us": e2.elapsed_time(e3) * 1e3 / 20,
+    wall_us = min(eager_wall, graph_wall)
+    return {"us_per_step": wall_us, "eager_step_us": eager_wall, "graph_step_us": graph_wall,
+            "eager_gpu_us": eager_gpu, "graph_gpu_us": graph_gpu, "kernel_us": kernel_us,
+            "one_launch": fused,
             "bytes_per_step": mean_bytes, "logical_gbs": mean_bytes / (wall_us * 1e-6) / 1e9,
             "hbm_frac_logical": mean_bytes / (wall_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+            "kernel_gbs": mean_bytes / (kernel_us * 1e-6) / 1e9,
+            "kernel_hbm_frac": mean_bytes / (kernel_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
             "batch": batch, "contexts": lengths, "steps": steps}
 
 

@@ -186,6 +186,40 @@ int moba_hip_decode_step(int* table, int table_width, int* lengths, const int* i
                          int dtype, void* k_cache, void* v_cache, int page_size, int Hkv, int D,
                          int chunk, void* means, int max_chunks, void* stream);
 
+/* 1 when moba_hip_decode_fused handles this shape: Hq/Hkv <= 16, D a
+ * multiple of 8 in [8,256], a page table of at most 2048 entries per row and
+ * a route width whose scratch fits LDS. */
+int moba_hip_decode_fused_supported(int Hq, int Hkv, int D, int width, int table_width);
+
+/* Whole decode for Nq query rows (one query per row) in ONE launch:
+ * routing (scores over the closed chunks c < min(pos / chunk, width), stable
+ * top-R per q head, selected [Nq,Hq,R+1] with slot 0 = pos / chunk, -1 pad;
+ * not written when dense), the paged attention over the union of the heads'
+ * chunks, out [Nq,Hq,D] and lse [Nq,Hq] fp32 natural log.
+ * pos_mode 0: positions [Nq] are given (read only; no table, length or pool
+ *             change).
+ * pos_mode 1: position = lengths[ids[row]] - 1 (prepared attend); the
+ *             page-table delta [2,Nq] (logical, physical; -1 = none; may be
+ *             null) is applied; positions written.
+ * pos_mode 2: position = lengths[ids[row]] (prepared step): as mode 1, plus the
+ *             new token k/v [Nq,Hkv,D] is scattered into the pool, the mean of
+ *             the chunk it closes is written to means (canonical order, as
+ *             moba_hip_block_means), and lengths advance by one.
+ * splits S in [1,64] workgroups per (row, kv head); workspaces part_o
+ * [Nq*Hq*S, D] and part_ml [Nq*Hq*S, 2] fp32; counters [Nq*Hkv + Nq] int32
+ * must be zero before the first launch and are left zero by every launch.
+ * width must be >= max(position) / chunk.  Launches on one counters buffer
+ * must not overlap.  Outputs are deterministic for a fixed S.
+ * Replaces _metadata + _append_kernel + _step_means + _route_kernel + top-k +
+ * _selected + _attention_kernel (prepared_decode.py:6-94, paged_decode.py:10-112). */
+int moba_hip_decode_fused(const void* q, const void* k, const void* v, int dtype, int Nq, int Hq,
+                          int Hkv, int D, void* k_cache, void* v_cache, int page_size, int* table,
+                          int table_width, int* lengths, const int* ids, int* positions,
+                          const int* delta, void* means, int max_chunks, int chunk, int width,
+                          int R, int dense, int pos_mode, int splits, int* selected,
+                          float* part_o, float* part_ml, int* counters, void* out, float* lse,
+                          void* stream);
+
 #ifdef __cplusplus
 }
 #endif

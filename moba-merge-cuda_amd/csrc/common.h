@@ -64,6 +64,17 @@ MOBA_DEV f32x16_t mfma32(const u16x8_t& a, const u16x8_t& b, const f32x16_t& c) 
   }
 }
 
+// 16x16x32 MFMA (A: row l%16, k (l/16)*8+e; D: column l%16, rows 4(l/16)+i).
+template <int DT>
+MOBA_DEV f32x4_t mfma16(const u16x8_t& a, const u16x8_t& b, const f32x4_t& c) {
+  if constexpr (DT == 0)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
 MOBA_DEV f32x16_t zero16() {
   f32x16_t z;
 #pragma unroll

@@ -35,17 +35,7 @@ using namespace moba;
 
 namespace {
 
-typedef float f32x4v __attribute__((ext_vector_type(4)));
-
-template <int DT>
-MOBA_DEV f32x4v mfma16(const u16x8_t& a, const u16x8_t& b, const f32x4v& c) {
-  if constexpr (DT == 0)
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
-  else
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
-                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
-}
+typedef f32x4_t f32x4v;
 
 constexpr int kWaves = 8;  // waves per attention workgroup
 constexpr int kMaxRemote = 8;

@@ -1,0 +1,608 @@
+// One-launch paged MoBA decode on gfx950.
+//
+// Replaces, for one query per row, the whole launch sequence of a decode step
+// of src/moba_opt/ops/prepared_decode.py:6-94 and src/moba_opt/ops/paged_decode.py:
+// page-table delta + position / length advance (_metadata), the scatter of
+// the new token (_append_kernel), the mean of the chunk the token closes
+// (_step_means), route scores + stable top-k + selected slots (_route_kernel,
+// _stable_topk, _selected) and the attention (_attention_kernel).
+//
+// Grid: (splits S, query rows x kv heads).  Every workgroup of a (query, kv
+// head) first recomputes the route of the group's G <= 16 q heads (the work
+// is tiny: G x closed chunks dot products against the stored means), giving
+// every workgroup the same union of selected chunks.  The union's tokens, cut
+// into 32-token blocks, are split evenly over the S workgroups; each
+// workgroup's 4 waves take its blocks round-robin: S^T = K Q^T on
+// v_mfma_f32_16x16x32 (16 tokens x the 16 heads, K straight from the page
+// pool, heads that did not select the block's chunk masked), O^T += V^T P^T
+// with V^T from a wave-private LDS tile by the transposed read.  The waves
+// merge in LDS into one (o, max, sum) partial per (head, split).  The last
+// workgroup of the (query, kv head) to arrive (device-scope counter) merges
+// the S partials in split order, so the result does not depend on arrival
+// order, and resets the counter for the next launch.
+//
+// Step mode: the new token's K/V are read from the input rows (so no
+// workgroup waits for the scatter); split 0 scatters them and applies the
+// page-table delta, the last split computes the closing chunk mean, and the
+// last workgroup of the query row advances its length.
+#include "common.h"
+#include "../../include/moba_hip.h"
+
+using namespace moba;
+
+namespace {
+
+constexpr int kFW = 4;          // waves per workgroup
+constexpr int kMaxSlots = 9;    // current chunk + up to 8 routed chunks
+constexpr int kTblMax = 2048;   // page-table entries staged in LDS
+
+struct FusedArgs {
+  const uint16_t* q;   // [Nq, Hq, D]
+  const uint16_t* k;   // [Nq, Hkv, D] new tokens (step mode)
+  const uint16_t* v;
+  uint16_t* kc;        // pool [pages, P, Hkv, D]
+  uint16_t* vc;
+  int Nq, Hq, Hkv, D, G, P, W, C, width, R, max_chunks, dense, pos_mode;
+  float scale_log2;
+  int* table;          // [B, W]
+  int* lengths;        // [B]
+  const int* ids;      // [Nq]
+  int* positions;      // [Nq] (read when pos_mode == 0, written otherwise)
+  const int* delta;    // [2, Nq] (logical slot, physical page) or null
+  uint16_t* means;     // [B, max_chunks, Hkv, D]
+  int* selected;       // [Nq, Hq, R + 1] or null
+  float* part_o;       // [Nq, Hq, S, D]
+  float* part_ml;      // [Nq, Hq, S, 2]
+  int* counters;       // [Nq * Hkv + Nq], zero between launches
+  uint16_t* out;       // [Nq, Hq, D]
+  float* lse;          // [Nq, Hq]
+};
+
+// Route scratch in dynamic LDS (ints / floats):
+//   sc[G * width] | umask[width + 1] | item_c[width + 1] | item_m[width + 1] |
+//   bp[width + 2] | sel[16 * kMaxSlots] | table row [kTblMax]
+inline size_t fused_route_lds(int G, int width) {
+  return sizeof(int) *
+         ((size_t)G * width + 3 * (size_t)(width + 1) + (width + 2) + 16 * kMaxSlots + kTblMax);
+}
+
+template <int DT, int DP>
+__global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
+  constexpr int NKS = DP / 32;  // 32-d k-steps of S^T
+  constexpr int NDB = DP / 16;  // 16-d blocks of O^T
+  constexpr int VS = DP + 8;
+  constexpr int STAGE = 32 * VS;  // per-wave V tile (elements)
+  constexpr int STAGE_BYTES = kFW * STAGE * 2;
+  constexpr int MERGE_BYTES = kFW * (16 * DP + 32) * 4;
+  constexpr int VLD = 32 * (DP / 8) / 64;  // 16-byte V chunks per lane per block
+  static_assert(80 * DP * 2 <= (STAGE_BYTES > MERGE_BYTES ? STAGE_BYTES : MERGE_BYTES),
+                "route staging must fit the V-tile / merge buffer");
+  __shared__ __attribute__((aligned(16))) unsigned char lds[STAGE_BYTES > MERGE_BYTES ? STAGE_BYTES : MERGE_BYTES];
+  extern __shared__ int dyn[];
+  __shared__ int s_info[8];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g4 = lane >> 4, c16 = lane & 15;
+  const int split = blockIdx.x, S = gridDim.x;
+  const int rowk = blockIdx.y, qrow = rowk / a.Hkv, kh = rowk % a.Hkv;
+  const int G = a.G, D = a.D, C = a.C, width = a.width;
+
+  if (tid == 0) {
+    const int sid = a.ids[qrow];
+    int p;
+    if (a.pos_mode == 0) {
+      p = a.positions[qrow];
+    } else {
+      const int len = a.lengths[sid];
+      p = a.pos_mode == 2 ? len : len - 1;
+    }
+    s_info[0] = sid;
+    s_info[1] = p;
+    s_info[2] = a.delta ? a.delta[qrow] : -1;
+    s_info[3] = a.delta ? a.delta[a.Nq + qrow] : -1;
+  }
+  __syncthreads();
+  const int sid = s_info[0], p = s_info[1], dl = s_info[2], dp = s_info[3];
+  const bool step = a.pos_mode == 2;
+  if (p < 0 || p / C > width) return;  // caller contract: width covers every position
+  const int* trow = a.table + (int64_t)sid * a.W;
+  // the row's page-table entries up to the query's page, staged in LDS
+  // (every lookup below reads LDS, so no global load ever waits behind the
+  // K/V stream); W <= kTblMax is a launch precondition
+  int* tbl = dyn + (G * width + 3 * (width + 1) + (width + 2) + 16 * kMaxSlots);
+  const int npg = min(p / a.P + 1, a.W);
+  for (int x0 = 0; x0 < npg; x0 += 4 * 64 * kFW) {
+    int t[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int x = x0 + tid + i * 64 * kFW;
+      t[i] = x < npg ? trow[x] : -1;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int x = x0 + tid + i * 64 * kFW;
+      if (x < npg) tbl[x] = t[i];
+    }
+  }
+  __syncthreads();
+  // page of logical slot `slot`; the page-table delta of this launch wins
+  auto page_at = [&](int slot) -> int { return slot == dl ? dp : tbl[slot]; };
+
+  // ---- side work of a step: scatter + table delta (split 0), closing mean (last split)
+  if (a.pos_mode != 0 && split == 0 && kh == 0 && tid == 0 && dl >= 0)
+    a.table[(int64_t)sid * a.W + dl] = dp;
+  if (step && split == 0) {
+    const int page = page_at(p / a.P);
+    if (page >= 0) {
+      const int64_t dst = (((int64_t)page * a.P + p % a.P) * a.Hkv + kh) * D;
+      const int64_t src = ((int64_t)qrow * a.Hkv + kh) * D;
+      for (int x = tid * 8; x < D; x += 64 * kFW * 8) {
+        st8(a.kc + dst + x, ld8(a.k + src + x));
+        st8(a.vc + dst + x, ld8(a.v + src + x));
+      }
+    }
+  }
+  if (step && split == S - 1 && (p + 1) % C == 0) {
+    // canonical order: lane j sums tokens j, j+64, ... of the chunk, then the tree
+    const int cc = p / C, nd8 = D / 8;
+    for (int item = w; item < nd8; item += kFW) {
+      const int d0 = item * 8;
+      float acc[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+      for (int t = cc * C + lane; t < (cc + 1) * C; t += 64) {
+        u16x8_t x;
+        if (t == p) {
+          x = ld8(a.k + ((int64_t)qrow * a.Hkv + kh) * D + d0);
+        } else {
+          const int pg = page_at(t / a.P);
+          if (pg < 0) continue;
+          x = ld8(a.kc + (((int64_t)pg * a.P + t % a.P) * a.Hkv + kh) * D + d0);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = acc[e] + to_f32<DT>(x[e]);
+      }
+      uint16_t res[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) res[e] = from_f32<DT>(canon_tree(acc[e]) / (float)C);
+      if (lane == 0) {
+        uint16_t* m = a.means + (((int64_t)sid * a.max_chunks + cc) * a.Hkv + kh) * D + d0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) m[e] = res[e];
+      }
+    }
+  }
+
+  // ---- route: scores, stable top-R per head, union of the chosen chunks
+  float* sc = reinterpret_cast<float*>(dyn);
+  int* umask = dyn + G * width;
+  int* item_c = umask + (width + 1);
+  int* item_m = item_c + (width + 1);
+  int* bp = item_m + (width + 1);
+  int* sel_s = bp + (width + 2);
+  const int cur = p / C;  // the current chunk (always attended, by every head)
+  const int all_heads = (int)((1u << G) - 1u);
+  const int S1 = a.R + 1;
+  for (int c = tid; c <= cur; c += 64 * kFW) umask[c] = (a.dense || c == cur) ? all_heads : 0;
+  for (int x = tid; x < G * S1; x += 64 * kFW) sel_s[x] = x % S1 == 0 ? cur : -1;
+  if (!a.dense) {
+    const int legal = min(cur, width);  // chunks c with (c + 1) * C <= p
+    // the group's q rows and 64 means rows at a time are staged in LDS with
+    // one burst of loads; each score is then a sequential fma chain over d
+    constexpr int RC = DP / 8;                  // 16-byte pieces per row
+    constexpr int NSTG = (64 * RC + 64 * kFW - 1) / (64 * kFW);
+    uint16_t* ms = reinterpret_cast<uint16_t*>(lds);  // [64][DP]
+    uint16_t* qs = ms + 64 * DP;                       // [16][DP]
+    for (int x = tid; x < G * RC; x += 64 * kFW) {
+      const int g = x / RC, j = x % RC;
+      st8(qs + g * DP + j * 8,
+          j * 8 < D ? ld8(a.q + ((int64_t)qrow * a.Hq + kh * G + g) * D + j * 8) : zero8());
+    }
+    for (int c0 = 0; c0 < legal; c0 += 64) {
+      const int nc = min(64, legal - c0);
+      u16x8_t stg[NSTG];
+#pragma unroll
+      for (int i = 0; i < NSTG; ++i) {
+        const int x = tid + i * 64 * kFW, cl = x / RC, j = x % RC;
+        stg[i] = (cl < nc && j * 8 < D)
+                     ? ld8(a.means + (((int64_t)sid * a.max_chunks + c0 + cl) * a.Hkv + kh) * D + j * 8)
+                     : zero8();
+      }
+#pragma unroll
+      for (int i = 0; i < NSTG; ++i) {
+        const int x = tid + i * 64 * kFW, cl = x / RC, j = x % RC;
+        if (cl < 64) st8(ms + cl * DP + j * 8, stg[i]);
+      }
+      __syncthreads();
+      for (int x = tid; x < G * nc; x += 64 * kFW) {
+        const int g = x / nc, cl = x % nc;
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < RC; ++j) {
+          if (j * 8 < D) {
+            const u16x8_t mv = ld8(ms + cl * DP + j * 8), qv = ld8(qs + g * DP + j * 8);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc = fmaf(to_f32<DT>(mv[e]), to_f32<DT>(qv[e]), acc);
+          }
+        }
+        sc[g * width + c0 + cl] = acc;
+      }
+      __syncthreads();
+    }
+    // stable top-R by rank: chunk c of head g takes slot 1 + rank, where rank
+    // counts the chunks ahead of it in (score desc, chunk asc) order; -inf
+    // and NaN scores are never selected.  Same picks as R rounds of "best
+    // candidate strictly after the previous pick".
+    for (int x = tid; x < G * legal; x += 64 * kFW) {
+      const int g = x / legal, c = x % legal;
+      const float* sg = sc + g * width;
+      const float v = sg[c];
+      if (!(v > -INFINITY)) continue;
+      int rank = 0;
+      for (int c2 = 0; c2 < legal && rank < a.R; ++c2) {
+        const float u = sg[c2];
+        rank += (u > v || (u == v && c2 < c)) ? 1 : 0;
+      }
+      if (rank < a.R) {
+        sel_s[g * S1 + 1 + rank] = c;
+        atomicOr(&umask[c], 1 << g);
+      }
+    }
+  }
+  __syncthreads();
+  if (!a.dense && split == 0 && a.selected != nullptr) {
+    for (int x = tid; x < G * S1; x += 64 * kFW) {
+      const int g = x / S1, j = x % S1;
+      a.selected[((int64_t)qrow * a.Hq + kh * G + g) * S1 + j] = sel_s[x];
+    }
+  }
+  // items: the union's chunks in ascending order with their head masks, and
+  // the prefix count of 32-token blocks
+  if (w == 0) {
+    int n = 0, nb = 0;
+    for (int c0 = 0; c0 <= cur; c0 += 64) {
+      const int c = c0 + lane;
+      const int m = c <= cur ? umask[c] : 0;
+      const uint64_t bal = __ballot(m != 0);
+      const int rank = n + __popcll(bal & ((1ull << lane) - 1ull));
+      const int ntok = c < cur ? C : p + 1 - cur * C;
+      int blocks = m != 0 ? (ntok + 31) / 32 : 0;
+      // inclusive scan of the block counts over the wave
+      int incl = blocks;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += y;
+      }
+      if (m != 0) {
+        item_c[rank] = c;
+        item_m[rank] = m;
+        bp[rank] = nb + incl - blocks;
+      }
+      n += __popcll(bal);
+      nb += __shfl(incl, 63, 64);
+    }
+    if (lane == 0) {
+      bp[n] = nb;
+      s_info[4] = n;
+      s_info[5] = nb;
+    }
+  }
+  __syncthreads();
+  const int n_items = s_info[4], NB = s_info[5];
+  const int b0 = (int)((int64_t)split * NB / S), b1 = (int)((int64_t)(split + 1) * NB / S);
+
+  // ---- attention over blocks [b0, b1)
+  uint16_t* Vs = reinterpret_cast<uint16_t*>(lds) + w * STAGE;
+  const bool head_ok = c16 < G;
+  const int h = kh * G + (head_ok ? c16 : 0);
+  u16x8_t qf[NKS];
+  {
+    const uint16_t* qp = a.q + ((int64_t)qrow * a.Hq + h) * D;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const int d = ks * 32 + g4 * 8;
+      qf[ks] = (head_ok && d < D) ? ld8(qp + d) : zero8();
+    }
+  }
+  f32x4_t oacc[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) oacc[db] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, lsum = 0.0f;
+
+  struct Blk { int t0, t_end, mask; };
+  auto block_info = [&](int b) -> Blk {
+    int lo = 0, hi = n_items - 1;  // last item with bp[i] <= b
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (bp[mid] <= b) lo = mid; else hi = mid - 1;
+    }
+    const int c = item_c[lo];
+    Blk r;
+    r.t0 = c * C + (b - bp[lo]) * 32;
+    r.t_end = min((c + 1) * C, p + 1);
+    r.mask = item_m[lo];
+    return r;
+  };
+  // K rows of tokens t0 + half*16 + c16 and the V rows of the block.  A row
+  // is (source, element offset): the new token of a step comes from the input
+  // row; tokens past the block end or on unmapped pages read as zero.
+  auto row_of = [&](int tok, bool& from_input) -> int64_t {
+    from_input = false;
+    if (tok >= 0 && step && tok == p) {
+      from_input = true;
+      return ((int64_t)qrow * a.Hkv + kh) * D;
+    }
+    const int pg = page_at(tok / a.P);
+    if (pg < 0) return -1;
+    return (((int64_t)pg * a.P + tok % a.P) * a.Hkv + kh) * D;
+  };
+  auto load = [&](const Blk& bk, u16x8_t (&kr)[2][NKS], u16x8_t (&vr)[VLD]) {
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int tok = bk.t0 + half * 16 + c16;
+      bool inp;
+      const int64_t base = tok < bk.t_end ? row_of(tok, inp) : -1;
+      const uint16_t* kp = inp ? a.k : a.kc;
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        const int d = ks * 32 + g4 * 8;
+        kr[half][ks] = (base >= 0 && d < D) ? ld8(kp + base + d) : zero8();
+      }
+    }
+#pragma unroll
+    for (int x = 0; x < VLD; ++x) {
+      const int id = lane + 64 * x, rr = id / (DP / 8), dc = (id % (DP / 8)) * 8;
+      const int tok = bk.t0 + rr;
+      bool inp;
+      const int64_t base = tok < bk.t_end ? row_of(tok, inp) : -1;
+      const uint16_t* vp = inp ? a.v : a.vc;
+      vr[x] = (base >= 0 && dc < D) ? ld8(vp + base + dc) : zero8();
+    }
+  };
+  auto compute = [&](const Blk& bk, const u16x8_t (&kr)[2][NKS], const u16x8_t (&vr)[VLD]) {
+    f32x4_t s4[2];
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      s4[half] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) s4[half] = mfma16<DT>(kr[half][ks], qf[ks], s4[half]);
+    }
+#pragma unroll
+    for (int x = 0; x < VLD; ++x) {
+      const int id = lane + 64 * x, rr = id / (DP / 8), dc = (id % (DP / 8)) * 8;
+      st8(&Vs[rr * VS + dc], vr[x]);
+    }
+    const bool on = head_ok && ((bk.mask >> c16) & 1);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int half = 0; half < 2; ++half)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int tok = bk.t0 + half * 16 + 4 * g4 + e;
+        const float xv = (on && tok < bk.t_end) ? s4[half][e] * a.scale_log2 : -INFINITY;
+        s4[half][e] = xv;
+        mx = fmaxf(mx, xv);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mn = fmaxf(m_run, mx);
+    const float ms = mn == -INFINITY ? 0.0f : mn;  // no finite score yet: all weights 0
+    const float alpha = fast_exp2(m_run - ms);
+    m_run = mn;
+    float pr[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      pr[e] = fast_exp2(s4[0][e] - ms);
+      pr[4 + e] = fast_exp2(s4[1][e] - ms);
+    }
+    float ps = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ps += pr[e];
+    lsum = lsum * alpha + ps;
+    const u16x8_t pv = pack8<DT>(pr);
+    // the V tile is private to this wave: order its LDS stores before the reads
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      // A = V^T (16 d x 32 tokens): column db*16 + c16, rows 4g4.. and 16+4g4..
+      const uint16_t* p0 = Vs + (4 * g4 + (c16 >> 2)) * VS + db * 16 + 4 * (c16 & 3);
+      const u16x4_t lo = ld_tr4(p0), hi = ld_tr4(p0 + 16 * VS);
+      u16x8_t av;
+      av[0] = lo[0]; av[1] = lo[1]; av[2] = lo[2]; av[3] = lo[3];
+      av[4] = hi[0]; av[5] = hi[1]; av[6] = hi[2]; av[7] = hi[3];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) oacc[db][e] *= alpha;
+      oacc[db] = mfma16<DT>(av, pv, oacc[db]);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  {
+    // ping-pong register buffers: block b + 4 loads while block b computes
+    int b = b0 + w;
+    if (b < b1) {
+      u16x8_t kA[2][NKS], vA[VLD], kB[2][NKS], vB[VLD];
+      Blk bA = block_info(b), bB;
+      load(bA, kA, vA);
+      __builtin_amdgcn_sched_barrier(0);
+      for (;;) {
+        const int bn = b + kFW;
+        if (bn < b1) {
+          bB = block_info(bn);
+          load(bB, kB, vB);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        compute(bA, kA, vA);
+        if (bn >= b1) break;
+        const int bn2 = bn + kFW;
+        if (bn2 < b1) {
+          bA = block_info(bn2);
+          load(bA, kA, vA);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        compute(bB, kB, vB);
+        if (bn2 >= b1) break;
+        b = bn2;
+      }
+    }
+  }
+  lsum += __shfl_xor(lsum, 16, 64);
+  lsum += __shfl_xor(lsum, 32, 64);
+
+  // ---- merge the 4 waves in LDS into this split's partial per head
+  __syncthreads();  // all V tiles consumed: the merge buffer aliases them
+  float* mrg = reinterpret_cast<float*>(lds);
+  {
+    float* wo = mrg + w * (16 * DP + 32);
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) wo[c16 * DP + db * 16 + 4 * g4 + e] = oacc[db][e];
+    if (g4 == 0) { wo[16 * DP + c16] = m_run; wo[16 * DP + 16 + c16] = lsum; }
+  }
+  __syncthreads();
+  for (int x = tid; x < G * D; x += 64 * kFW) {
+    const int g = x / D, d = x % D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < kFW; ++ww) {
+      const float* o = mrg + ww * (16 * DP + 32);
+      if (o[16 * DP + 16 + g] > 0.0f) M = fmaxf(M, o[16 * DP + g]);
+    }
+    float z = 0.0f, acc = 0.0f;
+#pragma unroll
+    for (int ww = 0; ww < kFW; ++ww) {
+      const float* o = mrg + ww * (16 * DP + 32);
+      const float l = o[16 * DP + 16 + g];
+      if (l > 0.0f) {
+        const float f = fast_exp2(o[16 * DP + g] - M);
+        z += l * f;
+        acc += o[g * DP + d] * f;
+      }
+    }
+    const int64_t entry = ((int64_t)qrow * a.Hq + kh * G + g) * S + split;
+    a.part_o[entry * D + d] = z > 0.0f ? acc / z : 0.0f;
+    if (d == 0) { a.part_ml[2 * entry] = M; a.part_ml[2 * entry + 1] = z; }
+  }
+
+  // ---- the last workgroup of this (query, kv head) merges the splits.  The
+  // barrier completes every thread's partial stores; one agent-scope release
+  // by thread 0 then publishes them (L2 writeback) before the arrival count,
+  // and the last arrival's agent-scope acquire makes all splits visible.
+  __syncthreads();
+  if (tid == 0) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    const bool last = atomicAdd(&a.counters[rowk], 1) == S - 1;
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    s_info[6] = last;
+  }
+  __syncthreads();
+  if (!s_info[6]) return;
+  // split weights in LDS: w[g][s] = z_s * 2^(m_s - M_g), one parallel load round
+  float* wts = reinterpret_cast<float*>(lds);   // [16][S]
+  float* gM = wts + 16 * S;                     // [16]
+  float* gZ = gM + 16;                          // [16]
+  for (int x = tid; x < G * S; x += 64 * kFW) {
+    const int64_t e = ((int64_t)qrow * a.Hq + kh * G + x / S) * S + x % S;
+    const float m = a.part_ml[2 * e], z = a.part_ml[2 * e + 1];
+    wts[x] = z > 0.0f ? m : -INFINITY;
+    wts[16 * S + 32 + x] = z;  // staged sums
+  }
+  __syncthreads();
+  if (tid < G) {
+    float M = -INFINITY;
+    for (int s = 0; s < S; ++s) M = fmaxf(M, wts[tid * S + s]);
+    float Z = 0.0f;
+    for (int s = 0; s < S; ++s) {
+      const float z = wts[16 * S + 32 + tid * S + s];
+      const float wgt = z > 0.0f ? z * fast_exp2(wts[tid * S + s] - M) : 0.0f;
+      wts[tid * S + s] = wgt;
+      Z += wgt;
+    }
+    gM[tid] = M;
+    gZ[tid] = Z;
+  }
+  __syncthreads();
+  for (int x = tid; x < G * D; x += 64 * kFW) {
+    const int g = x / D, d = x % D;
+    const int64_t row = (int64_t)qrow * a.Hq + kh * G + g;
+    const float* po = a.part_o + row * S * D + d;
+    const float* wg = wts + g * S;
+    float acc = 0.0f;
+#pragma unroll 8
+    for (int s = 0; s < S; ++s) acc += wg[s] * po[(int64_t)s * D];
+    a.out[row * D + d] = from_f32<DT>(acc / gZ[g]);
+    if (d == 0) a.lse[row] = (gM[g] + log2f(gZ[g])) * kLn2;
+  }
+  if (tid == 0) {
+    a.counters[rowk] = 0;
+    if (a.pos_mode != 0) {
+      // the row's last kv head finished: publish its position and advance its length
+      const int done = atomicAdd(&a.counters[a.Nq * a.Hkv + qrow], 1);
+      if (done == a.Hkv - 1) {
+        a.counters[a.Nq * a.Hkv + qrow] = 0;
+        a.positions[qrow] = p;
+        if (step) a.lengths[sid] = p + 1;
+      }
+    }
+  }
+}
+
+template <int DT, int DP>
+int launch_fused(const FusedArgs& a, int splits, size_t dyn, hipStream_t st) {
+  dim3 grid((unsigned)splits, (unsigned)(a.Nq * a.Hkv));
+  hipLaunchKernelGGL((fused_kernel<DT, DP>), grid, dim3(64 * kFW), dyn, st, a);
+  return moba_launch_status("decode_fused");
+}
+
+template <int DT>
+int dispatch_fused(const FusedArgs& a, int splits, size_t dyn, hipStream_t st) {
+  if (a.D <= 32) return launch_fused<DT, 32>(a, splits, dyn, st);
+  if (a.D <= 64) return launch_fused<DT, 64>(a, splits, dyn, st);
+  if (a.D <= 128) return launch_fused<DT, 128>(a, splits, dyn, st);
+  return launch_fused<DT, 256>(a, splits, dyn, st);
+}
+
+}  // namespace
+
+extern "C" int moba_hip_decode_fused_supported(int Hq, int Hkv, int D, int width, int table_width) {
+  if (Hkv < 1 || Hq % Hkv || Hq / Hkv > 16 || D % 8 || D < 8 || D > 256) return 0;
+  if (table_width < 1 || table_width > kTblMax) return 0;
+  return fused_route_lds(Hq / Hkv, width) <= 64 * 1024 ? 1 : 0;
+}
+
+extern "C" int moba_hip_decode_fused(const void* q, const void* k, const void* v, int dtype, int Nq,
+                                     int Hq, int Hkv, int D, void* k_cache, void* v_cache,
+                                     int page_size, int* table, int table_width, int* lengths,
+                                     const int* ids, int* positions, const int* delta, void* means,
+                                     int max_chunks, int chunk, int width, int R, int dense,
+                                     int pos_mode, int splits, int* selected, float* part_o,
+                                     float* part_ml, int* counters, void* out, float* lse,
+                                     void* stream) {
+  if (dtype != 0 && dtype != 1) { moba_set_error("decode_fused: dtype must be 0 (bf16) or 1 (fp16)"); return MOBA_ERR_ARG; }
+  if (!moba_hip_decode_fused_supported(Hq, Hkv, D, width, table_width)) {
+    moba_set_error("decode_fused: needs Hq/Hkv <= 16, head_dim a multiple of 8 in [8,256], a table width <= 2048 and a route width that fits LDS");
+    return MOBA_ERR_CAPACITY;
+  }
+  if (R < 0 || R + 1 > kMaxSlots) { moba_set_error("decode_fused: routed chunk count must be in [0,8]"); return MOBA_ERR_ARG; }
+  if (pos_mode < 0 || pos_mode > 2) { moba_set_error("decode_fused: pos_mode must be 0 (given), 1 (attend) or 2 (step)"); return MOBA_ERR_ARG; }
+  if (splits < 1 || splits > 64) { moba_set_error("decode_fused: splits must be in [1,64]"); return MOBA_ERR_ARG; }
+  if (page_size < 1 || chunk < 1 || width < 0 || Nq < 1) { moba_set_error("decode_fused: bad sizes"); return MOBA_ERR_ARG; }
+  if (pos_mode == 2 && (k == nullptr || v == nullptr)) { moba_set_error("decode_fused: step mode needs the new K/V rows"); return MOBA_ERR_ARG; }
+  FusedArgs a;
+  a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v;
+  a.kc = (uint16_t*)k_cache; a.vc = (uint16_t*)v_cache;
+  a.Nq = Nq; a.Hq = Hq; a.Hkv = Hkv; a.D = D; a.G = Hq / Hkv; a.P = page_size; a.W = table_width;
+  a.C = chunk; a.width = width; a.R = dense ? 0 : R; a.max_chunks = max_chunks; a.dense = dense;
+  a.pos_mode = pos_mode;
+  a.scale_log2 = kLog2e / sqrtf((float)D);
+  a.table = table; a.lengths = lengths; a.ids = ids; a.positions = positions; a.delta = delta;
+  a.means = (uint16_t*)means; a.selected = selected; a.part_o = part_o; a.part_ml = part_ml;
+  a.counters = counters; a.out = (uint16_t*)out; a.lse = lse;
+  const size_t dyn = fused_route_lds(a.G, width);
+  hipStream_t st = (hipStream_t)stream;
+  return dtype == 0 ? dispatch_fused<0>(a, splits, dyn, st) : dispatch_fused<1>(a, splits, dyn, st);
+}

@@ -250,6 +250,22 @@ class PagedKVCache:
         q = q.contiguous()
         gpu_ids, gpu_pos = self._metadata(ids, pos) if gpu_metadata is None else gpu_metadata
         max_hist = max(pos) // self.chunk_size
+        nq, hq, _ = q.shape
+        remote = 0 if dense else min(int(topk) - 1, self._candidate_count)
+        width = max(1, remote, max_hist)
+        if kernels.fused_supported(hq, self.num_kv_heads, self.head_dim, width,
+                                  self._table.shape[1]) \
+                and nq * hq * width < 2 ** 31:
+            # route + attention in one launch (positions given; nothing mutates)
+            work = kernels.FusedWork(nq, hq, self.num_kv_heads, self.head_dim, self.device)
+            selected = None if dense else torch.empty((nq, hq, remote + 1), dtype=torch.int32,
+                                                      device=self.device)
+            out = torch.empty_like(q)
+            lse = torch.empty(q.shape[:2], device=self.device, dtype=torch.float32)
+            kernels.fused(q, None, None, self.k_cache, self.v_cache, self._table, self._lengths,
+                          gpu_ids, gpu_pos, None, self._means, self.chunk_size, width, remote,
+                          dense, 0, selected, work, out, lse)
+            return DecodeResult(out, lse, selected, ids, pos)
         work = None if dense else self._route(q, gpu_ids, gpu_pos, topk, max_hist)
         out = torch.empty_like(q)
         lse = torch.empty(q.shape[:2], device=self.device, dtype=torch.float32)

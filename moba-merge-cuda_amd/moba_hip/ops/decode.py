@@ -81,3 +81,38 @@ def step(table, lengths, ids, positions, delta, k, v, kc, vc, chunk, means):
               ids.data_ptr(), positions.data_ptr(), delta.data_ptr(), b, k.data_ptr(),
               v.data_ptr(), DTYPE_CODE[k.dtype], kc.data_ptr(), vc.data_ptr(), kc.shape[1], hk, d,
               chunk, means.data_ptr(), means.shape[1], _lib.stream_of(k.device))
+
+
+def fused_supported(hq, hkv, d, width, table_width) -> bool:
+    return bool(_lib.load().moba_hip_decode_fused_supported(hq, hkv, d, width, table_width))
+
+
+def fused_splits(nq, hkv) -> int:
+    """Workgroups per (row, kv head): about two per CU over the whole launch."""
+    return max(1, min(64, -(-512 // (nq * hkv))))
+
+
+class FusedWork:
+    """Persistent workspaces of ``fused``: split partials and arrival counters
+    (zeroed once; every launch leaves them zero)."""
+    __slots__ = ("splits", "part_o", "part_ml", "counters")
+
+    def __init__(self, nq, hq, hkv, d, device, splits=None):
+        self.splits = splits or fused_splits(nq, hkv)
+        n = nq * hq * self.splits
+        self.part_o = torch.empty((n, d), dtype=torch.float32, device=device)
+        self.part_ml = torch.empty((n, 2), dtype=torch.float32, device=device)
+        self.counters = torch.zeros(nq * hkv + nq, dtype=torch.int32, device=device)
+
+
+def fused(q, k, v, kc, vc, table, lengths, ids, positions, delta, means, chunk, width, remote,
+          dense, pos_mode, selected, work: FusedWork, out, lse):
+    """One-launch decode (route + attention; step mode also appends)."""
+    nq, hq, d = q.shape
+    _lib.call("moba_hip_decode_fused", q.data_ptr(), _lib.ptr(k), _lib.ptr(v),
+              DTYPE_CODE[q.dtype], nq, hq, kc.shape[2], d, kc.data_ptr(), vc.data_ptr(),
+              kc.shape[1], table.data_ptr(), table.shape[1], lengths.data_ptr(), ids.data_ptr(),
+              positions.data_ptr(), _lib.ptr(delta), means.data_ptr(), means.shape[1], chunk,
+              width, remote, 1 if dense else 0, pos_mode, work.splits, _lib.ptr(selected),
+              work.part_o.data_ptr(), work.part_ml.data_ptr(), work.counters.data_ptr(),
+              out.data_ptr(), lse.data_ptr(), _lib.stream_of(q.device))

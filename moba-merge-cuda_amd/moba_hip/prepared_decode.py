@@ -5,11 +5,15 @@ arguments, ``step`` / ``attend`` / ``capture`` / ``close``, context-manager use,
 lifecycle errors and the aliasing rule that outputs are persistent workspaces
 overwritten by the next call).
 
-One step is a fixed launch sequence on the cache's stream, so it can be
-captured once as a graph (``torch.cuda.graph`` records HIP graphs on ROCm):
+One step is ONE launch of decode_fused (page-table delta, positions, route,
+stable top-k, paged attention, scatter of the new token, closing-chunk mean,
+length advance) when the shape allows (Hq/Hkv <= 16, head_dim a multiple of
+8); otherwise the fixed sequence
     decode_step (page-table delta + positions + scatter + closing-chunk mean)
     -> decode_route (scores + stable top-k + slot list + work list)
     -> paged_attention (+ its slot combine).
+Either way the work is on the cache's stream and can be captured once as a
+graph (``torch.cuda.graph`` records HIP graphs on ROCm).
 Host work per step is O(active batch) planning plus, only when a row starts a
 new page, one synchronous 2 x B int32 upload of the page-table delta.
 Every kernel of the sequence is from libmoba_hip.so; none issues a memset, so
@@ -69,6 +73,9 @@ class PreparedDecode:
             n = b * h * nslot
             self._part_o = torch.empty((n, d), device=dev, dtype=torch.float32)
             self._part_ml = torch.empty((n, 2), device=dev, dtype=torch.float32)
+            # one-launch step (route + attention + append) when the shape allows
+            self._fused = (kernels.FusedWork(b, h, cache.num_kv_heads, d, dev)
+                           if kernels.fused_supported(h, cache.num_kv_heads, d, width, cache._table.shape[1]) else None)
             self.gpu_ids = torch.tensor(self.ids, device=dev, dtype=torch.int32)
             self.positions = torch.empty(b, device=dev, dtype=torch.int32)
             self.delta = torch.full((2, b), -1, device=dev, dtype=torch.int32)
@@ -128,6 +135,14 @@ class PreparedDecode:
 
     def _compute(self, append):
         c = self.cache
+        if self._fused is not None:
+            kernels.fused(self.q, self.k if append else None, self.v if append else None,
+                          c.k_cache, c.v_cache, c._table, c._lengths, self.gpu_ids,
+                          self.positions, self.delta, c._means, c.chunk_size,
+                          self.scores.shape[-1], self.remote, self.dense, 2 if append else 1,
+                          None if self.dense else self.selected, self._fused, self.output,
+                          self.lse)
+            return
         if append:  # metadata + scatter + closing-chunk mean in one launch
             kernels.step(c._table, c._lengths, self.gpu_ids, self.positions, self.delta, self.k,
                          self.v, c.k_cache, c.v_cache, c.chunk_size, c._means)
