@@ -75,7 +75,7 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
   constexpr int STAGE_BYTES = kFW * STAGE * 2;
   constexpr int MERGE_BYTES = kFW * (16 * DP + 32) * 4;
   constexpr int VLD = 32 * (DP / 8) / 64;  // 16-byte V chunks per lane per block
-  static_assert(80 * DP * 2 <= (STAGE_BYTES > MERGE_BYTES ? STAGE_BYTES : MERGE_BYTES),
+  static_assert((64 * (DP + 8) + 16 * DP) * 2 <= (STAGE_BYTES > MERGE_BYTES ? STAGE_BYTES : MERGE_BYTES),
                 "route staging must fit the V-tile / merge buffer");
   __shared__ __attribute__((aligned(16))) unsigned char lds[STAGE_BYTES > MERGE_BYTES ? STAGE_BYTES : MERGE_BYTES];
   extern __shared__ int dyn[];
@@ -105,22 +105,68 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
   const bool step = a.pos_mode == 2;
   if (p < 0 || p / C > width) return;  // caller contract: width covers every position
   const int* trow = a.table + (int64_t)sid * a.W;
-  // the row's page-table entries up to the query's page, staged in LDS
-  // (every lookup below reads LDS, so no global load ever waits behind the
-  // K/V stream); W <= kTblMax is a launch precondition
+  // One burst of loads, all depending only on (sid, p): the row's page-table
+  // entries up to the query's page (every page lookup below then reads LDS,
+  // so no global load waits behind the K/V stream; W <= kTblMax is a launch
+  // precondition), the group's q rows and the first 64 closed-chunk means.
   int* tbl = dyn + (G * width + 3 * (width + 1) + (width + 2) + 16 * kMaxSlots);
   const int npg = min(p / a.P + 1, a.W);
-  for (int x0 = 0; x0 < npg; x0 += 4 * 64 * kFW) {
+  const int cur = p / C;  // the current chunk (always attended, by every head)
+  const int legal = a.dense ? 0 : min(cur, width);  // chunks c with (c + 1) * C <= p
+  constexpr int RC = DP / 8;                  // 16-byte pieces per row
+  constexpr int NSTG = (64 * RC + 64 * kFW - 1) / (64 * kFW);
+  constexpr int MS = DP + 8;                         // padded row: conflict-free 16-byte reads
+  uint16_t* ms = reinterpret_cast<uint16_t*>(lds);  // [64][MS] means rows
+  uint16_t* qs = ms + 64 * MS;                       // [16][DP] q rows
+  auto load_means = [&](int c0, u16x8_t (&stg)[NSTG]) {
+    const int nc = min(64, legal - c0);
+#pragma unroll
+    for (int i = 0; i < NSTG; ++i) {
+      const int x = tid + i * 64 * kFW, cl = x / RC, j = x % RC;
+      stg[i] = (cl < nc && j * 8 < D)
+                   ? ld8(a.means + (((int64_t)sid * a.max_chunks + c0 + cl) * a.Hkv + kh) * D + j * 8)
+                   : zero8();
+    }
+  };
+  auto store_means = [&](const u16x8_t (&stg)[NSTG]) {
+#pragma unroll
+    for (int i = 0; i < NSTG; ++i) {
+      const int x = tid + i * 64 * kFW, cl = x / RC, j = x % RC;
+      if (cl < 64) st8(ms + cl * MS + j * 8, stg[i]);
+    }
+  };
+  {
     int t[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int x = x0 + tid + i * 64 * kFW;
+      const int x = tid + i * 64 * kFW;
       t[i] = x < npg ? trow[x] : -1;
     }
+    constexpr int NQ = (16 * RC + 64 * kFW - 1) / (64 * kFW);
+    u16x8_t qv[NQ];
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      const int x = tid + i * 64 * kFW, qg = x / RC, qj = x % RC;
+      qv[i] = (!a.dense && qg < G && qj * 8 < D)
+                  ? ld8(a.q + ((int64_t)qrow * a.Hq + kh * G + qg) * D + qj * 8)
+                  : zero8();
+    }
+    u16x8_t stg[NSTG];
+    if (legal > 0) load_means(0, stg);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int x = x0 + tid + i * 64 * kFW;
+      const int x = tid + i * 64 * kFW;
       if (x < npg) tbl[x] = t[i];
+    }
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      const int x = tid + i * 64 * kFW, qg = x / RC, qj = x % RC;
+      if (!a.dense && qg < G) st8(qs + qg * DP + qj * 8, qv[i]);
+    }
+    if (legal > 0) store_means(stg);
+    for (int x0 = 4 * 64 * kFW; x0 < npg; x0 += 64 * kFW) {  // long rows
+      const int x = x0 + tid;
+      if (x < npg) tbl[x] = trow[x];
     }
   }
   __syncthreads();
@@ -179,55 +225,36 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
   int* item_m = item_c + (width + 1);
   int* bp = item_m + (width + 1);
   int* sel_s = bp + (width + 2);
-  const int cur = p / C;  // the current chunk (always attended, by every head)
   const int all_heads = (int)((1u << G) - 1u);
   const int S1 = a.R + 1;
   for (int c = tid; c <= cur; c += 64 * kFW) umask[c] = (a.dense || c == cur) ? all_heads : 0;
   for (int x = tid; x < G * S1; x += 64 * kFW) sel_s[x] = x % S1 == 0 ? cur : -1;
   if (!a.dense) {
-    const int legal = min(cur, width);  // chunks c with (c + 1) * C <= p
-    // the group's q rows and 64 means rows at a time are staged in LDS with
-    // one burst of loads; each score is then a sequential fma chain over d
-    constexpr int RC = DP / 8;                  // 16-byte pieces per row
-    constexpr int NSTG = (64 * RC + 64 * kFW - 1) / (64 * kFW);
-    uint16_t* ms = reinterpret_cast<uint16_t*>(lds);  // [64][DP]
-    uint16_t* qs = ms + 64 * DP;                       // [16][DP]
-    for (int x = tid; x < G * RC; x += 64 * kFW) {
-      const int g = x / RC, j = x % RC;
-      st8(qs + g * DP + j * 8,
-          j * 8 < D ? ld8(a.q + ((int64_t)qrow * a.Hq + kh * G + g) * D + j * 8) : zero8());
-    }
+    // each score is a sequential fma chain over d against LDS-staged rows
     for (int c0 = 0; c0 < legal; c0 += 64) {
       const int nc = min(64, legal - c0);
-      u16x8_t stg[NSTG];
-#pragma unroll
-      for (int i = 0; i < NSTG; ++i) {
-        const int x = tid + i * 64 * kFW, cl = x / RC, j = x % RC;
-        stg[i] = (cl < nc && j * 8 < D)
-                     ? ld8(a.means + (((int64_t)sid * a.max_chunks + c0 + cl) * a.Hkv + kh) * D + j * 8)
-                     : zero8();
+      if (c0 > 0) {  // the first 64 means rows came with the first burst
+        u16x8_t stg[NSTG];
+        load_means(c0, stg);
+        __syncthreads();  // the previous tile's scores are done
+        store_means(stg);
+        __syncthreads();
       }
-#pragma unroll
-      for (int i = 0; i < NSTG; ++i) {
-        const int x = tid + i * 64 * kFW, cl = x / RC, j = x % RC;
-        if (cl < 64) st8(ms + cl * DP + j * 8, stg[i]);
-      }
-      __syncthreads();
       for (int x = tid; x < G * nc; x += 64 * kFW) {
         const int g = x / nc, cl = x % nc;
         float acc = 0.0f;
 #pragma unroll
         for (int j = 0; j < RC; ++j) {
           if (j * 8 < D) {
-            const u16x8_t mv = ld8(ms + cl * DP + j * 8), qv = ld8(qs + g * DP + j * 8);
+            const u16x8_t mv = ld8(ms + cl * MS + j * 8), qv = ld8(qs + g * DP + j * 8);
 #pragma unroll
             for (int e = 0; e < 8; ++e) acc = fmaf(to_f32<DT>(mv[e]), to_f32<DT>(qv[e]), acc);
           }
         }
         sc[g * width + c0 + cl] = acc;
       }
-      __syncthreads();
     }
+    __syncthreads();
     // stable top-R by rank: chunk c of head g takes slot 1 + rank, where rank
     // counts the chunks ahead of it in (score desc, chunk asc) order; -inf
     // and NaN scores are never selected.  Same picks as R rounds of "best
@@ -238,9 +265,12 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
       const float v = sg[c];
       if (!(v > -INFINITY)) continue;
       int rank = 0;
-      for (int c2 = 0; c2 < legal && rank < a.R; ++c2) {
-        const float u = sg[c2];
-        rank += (u > v || (u == v && c2 < c)) ? 1 : 0;
+      for (int c0 = 0; c0 < legal && rank < a.R; c0 += 4) {
+        float u[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) u[i] = c0 + i < legal ? sg[c0 + i] : -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) rank += (u[i] > v || (u[i] == v && c0 + i < c)) ? 1 : 0;
       }
       if (rank < a.R) {
         sel_s[g * S1 + 1 + rank] = c;
@@ -526,15 +556,26 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
     gZ[tid] = Z;
   }
   __syncthreads();
-  for (int x = tid; x < G * D; x += 64 * kFW) {
-    const int g = x / D, d = x % D;
+  // 4 consecutive d per thread: 16-byte loads, up to 16 splits in flight
+  const int D4 = D / 4;
+  for (int x = tid; x < G * D4; x += 64 * kFW) {
+    const int g = x / D4, d = (x % D4) * 4;
     const int64_t row = (int64_t)qrow * a.Hq + kh * G + g;
-    const float* po = a.part_o + row * S * D + d;
+    const f32x4_t* po = reinterpret_cast<const f32x4_t*>(a.part_o + row * S * D + d);
     const float* wg = wts + g * S;
-    float acc = 0.0f;
-#pragma unroll 8
-    for (int s = 0; s < S; ++s) acc += wg[s] * po[(int64_t)s * D];
-    a.out[row * D + d] = from_f32<DT>(acc / gZ[g]);
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 16
+    for (int s = 0; s < S; ++s) {
+      const f32x4_t o = po[(int64_t)s * D4];
+      const float wv = wg[s];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] += wv * o[e];
+    }
+    const float iz = 1.0f / gZ[g];
+    u16x4_t r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = from_f32<DT>(acc[e] * iz);
+    *reinterpret_cast<u16x4_t*>(a.out + row * D + d) = r;
     if (d == 0) a.lse[row] = (gM[g] + log2f(gZ[g])) * kLn2;
   }
   if (tid == 0) {

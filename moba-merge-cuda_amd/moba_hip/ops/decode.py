@@ -105,14 +105,26 @@ class FusedWork:
         self.counters = torch.zeros(nq * hkv + nq, dtype=torch.int32, device=device)
 
 
+def fused_args(q, k, v, kc, vc, table, lengths, ids, positions, delta, means, chunk, width,
+               remote, dense, pos_mode, selected, work: FusedWork, out, lse):
+    """Argument tuple of one ``moba_hip_decode_fused`` launch, without the
+    stream (device pointers of the given tensors)."""
+    nq, hq, d = q.shape
+    return (q.data_ptr(), _lib.ptr(k), _lib.ptr(v), DTYPE_CODE[q.dtype], nq, hq, kc.shape[2], d,
+            kc.data_ptr(), vc.data_ptr(), kc.shape[1], table.data_ptr(), table.shape[1],
+            lengths.data_ptr(), ids.data_ptr(), positions.data_ptr(), _lib.ptr(delta),
+            means.data_ptr(), means.shape[1], chunk, width, remote, 1 if dense else 0, pos_mode,
+            work.splits, _lib.ptr(selected), work.part_o.data_ptr(), work.part_ml.data_ptr(),
+            work.counters.data_ptr(), out.data_ptr(), lse.data_ptr())
+
+
+def launch_fused(args, stream):
+    _lib.call("moba_hip_decode_fused", *args, stream)
+
+
 def fused(q, k, v, kc, vc, table, lengths, ids, positions, delta, means, chunk, width, remote,
           dense, pos_mode, selected, work: FusedWork, out, lse):
     """One-launch decode (route + attention; step mode also appends)."""
-    nq, hq, d = q.shape
-    _lib.call("moba_hip_decode_fused", q.data_ptr(), _lib.ptr(k), _lib.ptr(v),
-              DTYPE_CODE[q.dtype], nq, hq, kc.shape[2], d, kc.data_ptr(), vc.data_ptr(),
-              kc.shape[1], table.data_ptr(), table.shape[1], lengths.data_ptr(), ids.data_ptr(),
-              positions.data_ptr(), _lib.ptr(delta), means.data_ptr(), means.shape[1], chunk,
-              width, remote, 1 if dense else 0, pos_mode, work.splits, _lib.ptr(selected),
-              work.part_o.data_ptr(), work.part_ml.data_ptr(), work.counters.data_ptr(),
-              out.data_ptr(), lse.data_ptr(), _lib.stream_of(q.device))
+    launch_fused(fused_args(q, k, v, kc, vc, table, lengths, ids, positions, delta, means, chunk,
+                            width, remote, dense, pos_mode, selected, work, out, lse),
+                 _lib.stream_of(q.device))

@@ -76,6 +76,7 @@ class PreparedDecode:
             # one-launch step (route + attention + append) when the shape allows
             self._fused = (kernels.FusedWork(b, h, cache.num_kv_heads, d, dev)
                            if kernels.fused_supported(h, cache.num_kv_heads, d, width, cache._table.shape[1]) else None)
+            self._fused_args = None
             self.gpu_ids = torch.tensor(self.ids, device=dev, dtype=torch.int32)
             self.positions = torch.empty(b, device=dev, dtype=torch.int32)
             self.delta = torch.full((2, b), -1, device=dev, dtype=torch.int32)
@@ -106,6 +107,10 @@ class PreparedDecode:
             raise ValueError("cross-stream cache access is unsupported")
 
     def _input(self, tensor, target, name):
+        if tensor is target:  # the persistent workspace itself: shape/dtype/storage hold
+            if self.check_finite and not bool(torch.isfinite(tensor).all()):
+                raise ValueError(f"{name} contains NaN/Inf")
+            return
         if not isinstance(tensor, torch.Tensor) or tensor.shape != target.shape:
             raise ValueError(f"{name} must have fixed shape {tuple(target.shape)}")
         if tensor.device != target.device or tensor.dtype != target.dtype \
@@ -136,12 +141,18 @@ class PreparedDecode:
     def _compute(self, append):
         c = self.cache
         if self._fused is not None:
-            kernels.fused(self.q, self.k if append else None, self.v if append else None,
-                          c.k_cache, c.v_cache, c._table, c._lengths, self.gpu_ids,
-                          self.positions, self.delta, c._means, c.chunk_size,
-                          self.scores.shape[-1], self.remote, self.dense, 2 if append else 1,
-                          None if self.dense else self.selected, self._fused, self.output,
-                          self.lse)
+            if self._fused_args is None:  # every pointer is a persistent workspace
+                self._fused_args = {
+                    mode: kernels.fused_args(
+                        self.q, self.k if mode == 2 else None, self.v if mode == 2 else None,
+                        c.k_cache, c.v_cache, c._table, c._lengths, self.gpu_ids,
+                        self.positions, self.delta, c._means, c.chunk_size,
+                        self.scores.shape[-1], self.remote, self.dense, mode,
+                        None if self.dense else self.selected, self._fused, self.output,
+                        self.lse)
+                    for mode in (1, 2)}
+            kernels.launch_fused(self._fused_args[2 if append else 1],
+                                 torch.cuda.current_stream(c.device).cuda_stream)
             return
         if append:  # metadata + scatter + closing-chunk mean in one launch
             kernels.step(c._table, c._lengths, self.gpu_ids, self.positions, self.delta, self.k,
