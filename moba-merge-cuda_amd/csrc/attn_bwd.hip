@@ -111,8 +111,9 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a
     for (int qb = 0; qb < QB; ++qb) {
       const int local = (t - a.tile_off[e]) * (128 * QB) + wave * (32 * QB) + qb * 32 + qi;
       valid[qb] = local < cnt;
-      slot[qb] = valid[qb] ? a.rows[base + local] : 0;
-      const int sh = slot[qb] / a.R;
+      const int packed = valid[qb] ? a.rows[base + local] : 0;  // (row << 3) | j
+      const int sh = packed >> 3;
+      slot[qb] = sh * a.R + (packed & 7);
       s[qb] = sh / a.Hq;
       h[qb] = sh % a.Hq;
     }
@@ -360,7 +361,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
         return s < c_hi ? s * a.Hq + kh * G + g : -1;
       }
       const int local = (it - G * n_self) * BQ + qr;
-      return local < n_rem ? a.rows[rbase + local] / a.R : -1;
+      return local < n_rem ? a.rows[rbase + local] >> 3 : -1;
     };
 
     int nrow[NLD], nlrow = -1;

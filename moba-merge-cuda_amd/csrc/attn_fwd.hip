@@ -93,8 +93,9 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void fwd_kernel(FwdArgs 
     for (int qb = 0; qb < QB; ++qb) {
       const int local = (t - a.tile_off[e]) * (128 * QB) + wave * (32 * QB) + qb * 32 + qi;
       valid[qb] = local < cnt;
-      slot[qb] = valid[qb] ? a.rows[base + local] : 0;
-      const int sh = slot[qb] / a.R;
+      const int packed = valid[qb] ? a.rows[base + local] : 0;  // (row << 3) | j
+      const int sh = packed >> 3;
+      slot[qb] = sh * a.R + (packed & 7);
       s[qb] = sh / a.Hq;
       h[qb] = sh % a.Hq;
     }

@@ -209,7 +209,7 @@ __global__ __launch_bounds__(1024) void expert_scan_kernel(const int* __restrict
   if (threadIdx.x == 0) { row_off[E] = carry_r; tile_off[E] = carry_t; }
 }
 
-// Ordered compaction: rows[row_off[e] + rank] = (s*Hq + h)*R + j.
+// Ordered compaction: rows[row_off[e] + rank] = ((s*Hq + h) << 3) | j (R <= 8).
 __global__ __launch_bounds__(256) void expert_fill_kernel(
     const int* __restrict__ sel, int Hq, int Hkv, int R, const int* __restrict__ cu_chunk,
     const int* __restrict__ chunk_batch, const int* __restrict__ cu_seqlens,
@@ -235,7 +235,7 @@ __global__ __launch_bounds__(256) void expert_fill_kernel(
     __syncthreads();
     int off = out;
     for (int k2 = 0; k2 < w; ++k2) off += wtot[k2];
-    if (slot >= 0) rows[off + before] = ((s * Hq) + h) * R + slot;
+    if (slot >= 0) rows[off + before] = (((s * Hq) + h) << 3) | slot;
     const int tot = wtot[0] + wtot[1] + wtot[2] + wtot[3];
     __syncthreads();
     out += tot;
@@ -293,7 +293,8 @@ extern "C" int moba_hip_pack_experts(const int* sel, int T, int Hq, int Hkv, int
                                      int* rows, void* stream) {
   (void)T;
   if (F <= 0) return MOBA_OK;
-  if ((int64_t)T * Hq * R >= (1ll << 31)) { moba_set_error("pack_experts: T*Hq*R exceeds int32"); return MOBA_ERR_ARG; }
+  if ((int64_t)T * Hq * R >= (1ll << 31) || (int64_t)T * Hq >= (1ll << 28)) { moba_set_error("pack_experts: T*Hq*R exceeds int32 or T*Hq exceeds 2^28"); return MOBA_ERR_ARG; }
+  if (R > 8) { moba_set_error("pack_experts: at most 8 remote chunks per query"); return MOBA_ERR_ARG; }
   hipStream_t st = (hipStream_t)stream;
   const int E = F * Hkv;
   hipLaunchKernelGGL(expert_count_kernel, dim3(E), dim3(256), 0, st, sel, Hq, Hkv, R, cu_chunk,

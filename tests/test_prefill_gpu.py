@@ -61,7 +61,7 @@ def test_routing_bit_exact(cuda_device, hq, hkv, dim, lens, chunk, topk, dtype, 
     counts = rt.counts.cpu().numpy()
     rows = rt.rows.cpu().numpy()[: counts.sum()]
     R = remote
-    expect = sorted(((s * hq + h) * R + j) for s in range(q.shape[0]) for h in range(hq)
+    expect = sorted((((s * hq + h) << 3) | j) for s in range(q.shape[0]) for h in range(hq)
                     for j in range(R) if sel[s, h, j] >= 0)
     assert sorted(rows.tolist()) == expect
 
