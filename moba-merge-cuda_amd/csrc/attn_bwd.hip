@@ -306,7 +306,7 @@ template <int DP> constexpr int dkdv_qb() { return DP <= 128 ? 2 : 1; }
 template <int DT, int DP>
 __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
   constexpr int QB = dkdv_qb<DP>();
-  constexpr int QS = DP + 8, NKS = DP / 16, NDB = DP / 32;
+  constexpr int QS = DP + 16, NKS = DP / 16, NDB = DP / 32;
   constexpr int BQ = 32 * QB;                 // query rows per tile
   constexpr int NLD = (BQ * DP / 8 + 511) / 512;
   constexpr int WKEYS = kDkdvPairKeys;        // keys per wave pair
