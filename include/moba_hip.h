@@ -99,6 +99,9 @@ int moba_hip_prefill_fwd(const void* q, const void* k, const void* v, int dtype,
  * (dtype) are fully written (every key belongs to exactly one kv tile).
  * parts selects the launches: 1 = Delta and dq (query-major kernels), 2 = dk/dv
  * (key-major kernel, needs the Delta of a parts-1 call), 3 = both in order.
+ * kv_splits in [1,16]: each key tile's query rows are split over that many
+ * workgroups (for few kv heads); when > 1, part_dkv [kv_splits*2*T*Hkv*D]
+ * fp32 is a workspace and D must be a multiple of 8.
  * Deterministic: no atomics, fixed reduction order. */
 int moba_hip_prefill_bwd(const void* q, const void* k, const void* v, const void* out,
                          const void* dout, const float* lse, int dtype, int T, int Hq, int Hkv,
@@ -107,7 +110,7 @@ int moba_hip_prefill_bwd(const void* q, const void* k, const void* v, const void
                          int R, const int* filtered, int E, const int* tile_off,
                          const int* row_off, const int* counts, const int* rows,
                          int max_remote_tiles, float* delta, float* part_dq, void* dq, void* dk,
-                         void* dv, int parts, void* stream);
+                         void* dv, int parts, int kv_splits, float* part_dkv, void* stream);
 
 /* ----------------------------------------------------------------- decode */
 

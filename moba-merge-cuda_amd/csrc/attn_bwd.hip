@@ -48,6 +48,8 @@ struct BwdArgs {
   const int* rows;
   float* delta;
   float* part_dq;
+  float* part_dkv;   // [kv_splits][2][T, Hkv, D] fp32 when kv_splits > 1
+  int kv_splits;
   uint16_t* dq;
   uint16_t* dk;
   uint16_t* dv;
@@ -354,6 +356,9 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
     const int n_rem = e >= 0 ? a.counts[e] : 0;
     const int rbase = e >= 0 ? a.row_off[e] : 0;
     const int n_tiles = G * n_self + (n_rem + BQ - 1) / BQ;
+    // row split: workgroup y of gridDim.y takes a contiguous share of the tiles
+    const int it_lo = (int)((int64_t)n_tiles * blockIdx.y / gridDim.y);
+    const int it_hi = (int)((int64_t)n_tiles * (blockIdx.y + 1) / gridDim.y);
 
     auto row_of = [&](int it, int qr) -> int {  // row index s*Hq+h, or -1
       if (it < G * n_self) {
@@ -399,16 +404,16 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
     };
 
     const float c2 = a.scale_log2;
-    if (n_tiles > 0) {
-      fetch_rows(0);
+    if (it_lo < it_hi) {
+      fetch_rows(it_lo);
       gload();
       lstore(0);
-      fetch_rows(1);
+      fetch_rows(it_lo + 1);
     }
     __syncthreads();
-    for (int it = 0; it < n_tiles; ++it) {
-      const int buf = it & 1;
-      if (it + 1 < n_tiles) {
+    for (int it = it_lo; it < it_hi; ++it) {
+      const int buf = (it - it_lo) & 1;
+      if (it + 1 < it_hi) {
         gload();
         fetch_rows(it + 2);
       }
@@ -484,11 +489,28 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
               acc[i] = mfma32<DT>(op[qb][t], ld_tr_operand(B2, QS, qb * 32 + t * 16, i * 32, lane),
                                   acc[i]);
       }
-      if (it + 1 < n_tiles) lstore(buf ^ 1);
+      if (it + 1 < it_hi) lstore(buf ^ 1);
       __syncthreads();
     }
 
-    // D-layout: lane holds column d = i*32 + qi, keys 8j + 4hh + r.
+    // D-layout: lane holds column d = i*32 + qi, keys 8j + 4hh + r.  With a
+    // row split the fp32 partial goes to part_dkv[(split, dk|dv)] for the
+    // fixed-order reduction.
+    if (gridDim.y > 1) {
+      const int64_t n = (int64_t)a.T * a.Hkv * D;
+      float* pdst = a.part_dkv + ((int64_t)blockIdx.y * 2 + (ROLE_P ? 1 : 0)) * n;
+#pragma unroll
+      for (int i = 0; i < NDB; ++i) {
+        const int d = i * 32 + qi;
+        if (d >= D) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = wkey0 + 8 * (r >> 2) + 4 * hh + (r & 3);
+          if (key < c_hi) pdst[((int64_t)key * a.Hkv + kh) * D + d] = acc[i][r];
+        }
+      }
+      return;
+    }
     uint16_t* dst = ROLE_P ? a.dv : a.dk;
     const float osc = ROLE_P ? 1.0f : a.scale;
 #pragma unroll
@@ -505,6 +527,29 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
   if (role_p) body(std::true_type{}); else body(std::false_type{});
 }
 
+// dK / dV from the row-split partials, summed in split order.
+template <int DT>
+__global__ __launch_bounds__(256) void dkdv_reduce_kernel(const float* __restrict__ part, int splits,
+                                                          int64_t n4, float scale,
+                                                          uint16_t* __restrict__ dk,
+                                                          uint16_t* __restrict__ dv) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= 2 * n4) return;
+  const int which = i >= n4;  // 0 = dK, 1 = dV
+  const int64_t j = which ? i - n4 : i;
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < splits; ++s) {
+    const f32x4_t x = reinterpret_cast<const f32x4_t*>(part)[(int64_t)(2 * s + which) * n4 + j];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] += x[e];
+  }
+  const float sc = which ? 1.0f : scale;
+  u16x4_t r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) r[e] = from_f32<DT>(acc[e] * sc);
+  reinterpret_cast<u16x4_t*>(which ? dv : dk)[j] = r;
+}
+
 template <int DT, int DP>
 int launch_bwd(const BwdArgs& a, int n_self, int n_kv, int max_remote, int parts, hipStream_t st) {
   const int64_t rows = (int64_t)a.T * a.Hq;
@@ -518,7 +563,12 @@ int launch_bwd(const BwdArgs& a, int n_self, int n_kv, int max_remote, int parts
   }
   if ((parts & 2) && n_kv > 0) {
     // 4 wave pairs x kDkdvPairKeys keys per workgroup; the host's key tiles match
-    hipLaunchKernelGGL((dkdv_kernel<DT, DP>), dim3(n_kv), dim3(512), 0, st, a);
+    hipLaunchKernelGGL((dkdv_kernel<DT, DP>), dim3(n_kv, a.kv_splits), dim3(512), 0, st, a);
+    if (a.kv_splits > 1) {
+      const int64_t n4 = (int64_t)a.T * a.Hkv * a.D / 4;
+      hipLaunchKernelGGL(dkdv_reduce_kernel<DT>, dim3((unsigned)((2 * n4 + 255) / 256)), dim3(256), 0,
+                         st, a.part_dkv, a.kv_splits, n4, a.scale, a.dk, a.dv);
+    }
   }
   return moba_launch_status("prefill_bwd");
 }
@@ -541,12 +591,13 @@ extern "C" int moba_hip_prefill_bwd(const void* q, const void* k, const void* v,
                                     int E, const int* tile_off, const int* row_off,
                                     const int* counts, const int* rows, int max_remote_tiles,
                                     float* delta, float* part_dq, void* dq, void* dk, void* dv,
-                                    int parts, void* stream) {
+                                    int parts, int kv_splits, float* part_dkv, void* stream) {
   if (dtype != 0 && dtype != 1) { moba_set_error("prefill_bwd: dtype must be 0 (bf16) or 1 (fp16)"); return MOBA_ERR_ARG; }
   if (D < 8 || D > 256 || D % 8) { moba_set_error("prefill_bwd: head_dim must be a multiple of 8 in [8,256]"); return MOBA_ERR_ARG; }
   if (Hq < 1 || Hkv < 1 || Hq % Hkv) { moba_set_error("prefill_bwd: Hq must be a positive multiple of Hkv"); return MOBA_ERR_ARG; }
   if (R < 0 || R > 8) { moba_set_error("prefill_bwd: remote count must be in [0,8]"); return MOBA_ERR_ARG; }
   if (parts < 1 || parts > 3) { moba_set_error("prefill_bwd: parts must be 1 (dq), 2 (dk/dv) or 3 (both)"); return MOBA_ERR_ARG; }
+  if (kv_splits < 1 || kv_splits > 16 || (kv_splits > 1 && (part_dkv == nullptr || D % 8))) { moba_set_error("prefill_bwd: kv_splits must be in [1,16], with a part_dkv workspace when > 1"); return MOBA_ERR_ARG; }
   BwdArgs a;
   a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v;
   a.out = (const uint16_t*)out; a.dout = (const uint16_t*)dout; a.lse = lse;
@@ -555,7 +606,7 @@ extern "C" int moba_hip_prefill_bwd(const void* q, const void* k, const void* v,
   a.cu_chunk = cu_chunk; a.self_tiles = self_tiles; a.kv_tiles = kv_tiles;
   a.sel = sel; a.R = R; a.filtered = filtered; a.E = E;
   a.tile_off = tile_off; a.row_off = row_off; a.counts = counts; a.rows = rows;
-  a.delta = delta; a.part_dq = part_dq;
+  a.delta = delta; a.part_dq = part_dq; a.part_dkv = part_dkv; a.kv_splits = kv_splits;
   a.dq = (uint16_t*)dq; a.dk = (uint16_t*)dk; a.dv = (uint16_t*)dv;
   hipStream_t st = (hipStream_t)stream;
   const int mr = R > 0 ? max_remote_tiles : 0;

@@ -79,6 +79,10 @@ class PrefillPlan:
         fidx = {c: i for i, c in enumerate(filtered)}
         self.kv_tiles_list = self._kv_tile_order(att_chunk, fidx, cu, chunk_batch, cu_chunk)
         self.n_kv_tiles = len(self.kv_tiles_list) // 4
+        # few kv heads leave too few key tiles to fill the chip: split each
+        # tile's query rows over several workgroups (fp32 partials + reduce)
+        self.kv_splits = (max(1, min(8, 1024 // max(1, self.n_kv_tiles)))
+                          if head_dim % 8 == 0 else 1)
         kv_flat = self.kv_tiles_list
 
         parts = OrderedDict(
@@ -227,12 +231,15 @@ def backward(plan: PrefillPlan, q, k, v, out, lse, dout, rt: RouteResult | None)
             _lib.ptr(rt.counts) if R else None, _lib.ptr(rt.rows) if R else None,
             plan.max_remote_tiles if R else 0, delta.data_ptr(), _lib.ptr(part_dq),
             dq.data_ptr(), dk.data_ptr(), dv.data_ptr()]
+    ks = plan.kv_splits
+    part_dkv = (torch.empty(ks * 2 * T * plan.hkv * d, dtype=torch.float32, device=dev)
+                if ks > 1 else None)
     st = _lib.stream_of(dev)
-    _lib.call("moba_hip_prefill_bwd", *args, 1, st)
+    _lib.call("moba_hip_prefill_bwd", *args, 1, ks, _lib.ptr(part_dkv), st)
     events = DKDV_EVENTS
     if events is not None:
         events[0].record()
-    _lib.call("moba_hip_prefill_bwd", *args, 2, st)
+    _lib.call("moba_hip_prefill_bwd", *args, 2, ks, _lib.ptr(part_dkv), st)
     if events is not None:
         events[1].record()
     return dq, dk, dv
