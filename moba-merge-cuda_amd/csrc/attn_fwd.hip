@@ -27,6 +27,8 @@
 // Each K / V^T fragment read from LDS feeds the MFMAs of both query blocks, and
 // the next K/V tile is prefetched into registers while the current one computes.
 // so every per-query quantity (running max, sum, rescale) is lane-uniform.
+#include <type_traits>
+
 #include "common.h"
 #include "../../include/moba_hip.h"
 
@@ -61,12 +63,18 @@ constexpr float kRescaleSlack = 8.0f;  // log2 headroom before O is rescaled
 
 template <int DT, int DP, bool REMOTE, int QB>
 __global__ __launch_bounds__(256, attn_occupancy<DP>()) void fwd_kernel(FwdArgs a) {
-  constexpr int KS = DP + 8;    // row stride (elements) of the K and V tiles
   constexpr int NKS = DP / 16;  // k-steps of the QK^T contraction
   constexpr int NDB = DP / 32;  // 32-row d blocks of O^T
-  constexpr int NLD = kBN * DP / 8 / 256;  // 16-byte chunks per thread per operand
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kBN * KS];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][kBN * KS];
+  constexpr int TILE = kBN * DP;           // elements of one K or V tile
+  constexpr int NB = DP / 8;                // 16-byte blocks per tile row
+  constexpr int NDMA = kBN * NB / 256;      // 16-byte blocks per thread per tile
+  // Two stages of K and V tiles in the swz<DP> layout, filled straight from
+  // HBM by buffer loads into LDS.  Separate arrays let the compiler see that
+  // reads of one stage never wait on the loads in flight into the other.
+  __shared__ __attribute__((aligned(16))) uint16_t K0[TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t V0[TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t K1[TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t V1[TILE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int qi = lane & 31, hh = lane >> 5;
@@ -126,26 +134,46 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void fwd_kernel(FwdArgs 
     }
   }
 
-  u16x8_t kr[NLD], vr[NLD];
-  auto gload = [&](int kt0) {
+  // Tile loads: block j of a tile (row j / NB, physical block j % NB) comes
+  // from logical column block (j % NB) ^ f(row); thread (wave w, lane l)
+  // loads blocks (n * 4 + w) * 64 + l.  Offsets are relative to key k_lo of
+  // head kh, so they are the same for every tile; the tile advance goes in the
+  // scalar offset.  Rows past k_hi lie beyond num_records and load zeros;
+  // column blocks past D are never loaded (zeroed once below).
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  uint32_t voff[NDMA];
+  bool vok[NDMA];
 #pragma unroll
-    for (int i = 0; i < NLD; ++i) {
-      const int id = tid + i * 256, key = id / (DP / 8), dc = (id % (DP / 8)) * 8;
-      const int kg = kt0 + key;
-      const bool ok = kg < k_hi && dc < D;
-      const int64_t off = ((int64_t)kg * a.Hkv + kh) * D + dc;
-      kr[i] = ok ? ld8(a.k + off) : zero8();
-      vr[i] = ok ? ld8(a.v + off) : zero8();
+  for (int n = 0; n < NDMA; ++n) {
+    const int j = (n * 4 + wave_s) * 64 + lane, row = j / NB;
+    const int col = swz<DP>(row, (j % NB) * 8) - row * DP;  // swizzle is an involution
+    voff[n] = (uint32_t)(((row * a.Hkv + kh) * D + col) * 2);
+    vok[n] = col < D;
+  }
+  const int n_keys = k_hi - k_lo;
+  const uint32_t nrec = (uint32_t)((((int64_t)(n_keys - 1) * a.Hkv + kh + 1) * D) * 2);
+  const uint16_t* kbase = a.k + (int64_t)k_lo * a.Hkv * D;
+  const uint16_t* vbase = a.v + (int64_t)k_lo * a.Hkv * D;
+  const uint32_t tile_bytes = (uint32_t)(kBN * a.Hkv * D * 2);
+  auto dma = [&](uint16_t* Kd, uint16_t* Vd, int it) {
+    const uint32_t soff = (uint32_t)it * tile_bytes;
+#pragma unroll
+    for (int n = 0; n < NDMA; ++n) {
+      if (vok[n]) {
+        load_lds16(make_rsrc(kbase, nrec), Kd + (n * 4 + wave_s) * 64 * 8, voff[n], soff);
+        load_lds16(make_rsrc(vbase, nrec), Vd + (n * 4 + wave_s) * 64 * 8, voff[n], soff);
+      }
     }
   };
-  auto lstore = [&](int buf) {
+  if (D < DP) {  // column blocks past D stay zero for the whole kernel
 #pragma unroll
-    for (int i = 0; i < NLD; ++i) {
-      const int id = tid + i * 256, key = id / (DP / 8), dc = (id % (DP / 8)) * 8;
-      st8(&Ks[buf][key * KS + dc], kr[i]);
-      st8(&Vs[buf][key * KS + dc], vr[i]);
+    for (int n = 0; n < NDMA; ++n) {
+      const int j = (n * 4 + wave) * 64 + lane;
+      st8(K0 + j * 8, zero8()); st8(V0 + j * 8, zero8());
+      st8(K1 + j * 8, zero8()); st8(V1 + j * 8, zero8());
     }
-  };
+    __syncthreads();
+  }
 
   f32x16_t oacc[QB][NDB];
 #pragma unroll
@@ -157,14 +185,25 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void fwd_kernel(FwdArgs 
   for (int qb = 0; qb < QB; ++qb) { m_run[qb] = -INFINITY; lsum[qb] = 0.0f; }
   const float c2 = a.scale_log2;
 
-  const int ntiles = (k_hi - k_lo + kBN - 1) / kBN;
-  gload(k_lo);
-  lstore(0);
-  __syncthreads();
-  for (int it = 0; it < ntiles; ++it) {
-    const int kt0 = k_lo + it * kBN, buf = it & 1;
-    if (it + 1 < ntiles) gload(kt0 + kBN);
+  // Lane-constant swizzled LDS offsets (elements): the rows this lane reads
+  // differ from these by multiples of 16, which the swizzle ignores.
+  int kofs[NKS], vofs[NDB][2];
+#pragma unroll
+  for (int ks = 0; ks < NKS; ++ks) kofs[ks] = swz<DP>(qi, ks * 16 + hh * 8);
+  {
+    const int sub = lane & 15, r = 4 * hh + (sub >> 2);
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const int col = db * 32 + ((lane >> 4) & 1) * 16 + 4 * (sub & 3);
+      vofs[db][0] = swz<DP>(r, col);
+      vofs[db][1] = swz<DP>(r + 8, col);
+    }
+  }
 
+  const int ntiles = (n_keys + kBN - 1) / kBN;
+  auto tile = [&](const uint16_t* Kb, const uint16_t* Vb, const int it, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    const int kt0 = k_lo + it * kBN;
     f32x16_t sacc[QB][2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
@@ -172,13 +211,12 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void fwd_kernel(FwdArgs 
       for (int qb = 0; qb < QB; ++qb) sacc[qb][kb] = zero16();
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {
-        const u16x8_t av = ld8(&Ks[buf][(kb * 32 + qi) * KS + ks * 16 + hh * 8]);
+        const u16x8_t av = ld8(Kb + kb * 32 * DP + kofs[ks]);
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) sacc[qb][kb] = mfma32<DT>(av, qf[qb][ks], sacc[qb][kb]);
       }
     }
-    const bool need_mask = (kt0 + kBN > k_hi) || (!REMOTE && kt0 + kBN - 1 > s_wave0);
-    if (need_mask) {
+    if constexpr (MASK) {
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
@@ -203,7 +241,7 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void fwd_kernel(FwdArgs 
       // 2^8 of it (p <= 256 is exact enough in bf16/fp32); O, l and the final
       // normalisation all use the same reference so the result is unchanged.
       const bool up = mx > m_run[qb] + kRescaleSlack;
-      if (__any(up)) {
+      if (__any(up)) [[unlikely]] {
         const float mn = up ? mx : m_run[qb];
         const float alpha = fast_exp2(m_run[qb] - mn);
         lsum[qb] *= alpha;
@@ -212,6 +250,7 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void fwd_kernel(FwdArgs 
 #pragma unroll
           for (int r = 0; r < 16; ++r) oacc[qb][db][r] *= alpha;
         m_run[qb] = mn;
+        __builtin_amdgcn_sched_barrier(0);
       }
       const float nm = -m_run[qb];
       float ps = 0.0f;
@@ -234,13 +273,38 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void fwd_kernel(FwdArgs 
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-          const u16x8_t av = ld_tr_operand(Vs[buf], KS, kb * 32 + t * 16, db * 32, lane);
+          const uint16_t* vb = Vb + (kb * 32 + t * 16) * DP;
+          const u16x4_t x0 = ld_tr4(vb + vofs[db][0]), x1 = ld_tr4(vb + vofs[db][1]);
+          u16x8_t av;
+          av[0] = x0[0]; av[1] = x0[1]; av[2] = x0[2]; av[3] = x0[3];
+          av[4] = x1[0]; av[5] = x1[1]; av[6] = x1[2]; av[7] = x1[3];
 #pragma unroll
           for (int qb = 0; qb < QB; ++qb) oacc[qb][db] = mfma32<DT>(av, pv[qb][kb][t], oacc[qb][db]);
         }
-    if (it + 1 < ntiles) lstore(buf ^ 1);
-    __syncthreads();
+  };
+  // vmcnt(0) with the other counters left alone, then a workgroup barrier:
+  // this wave's tile loads have landed, and after the barrier every wave's.
+  auto stage_sync = [&]() {
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __builtin_amdgcn_s_barrier();
+  };
+  auto run = [&](const uint16_t* Kb, const uint16_t* Vb, int it) {
+    const int kt0 = k_lo + it * kBN;
+    const bool need_mask = (kt0 + kBN > k_hi) || (!REMOTE && kt0 + kBN - 1 > s_wave0);
+    if (need_mask) tile(Kb, Vb, it, std::true_type{}); else tile(Kb, Vb, it, std::false_type{});
+  };
+  dma(K0, V0, 0);
+  stage_sync();
+  for (int it = 0; it < ntiles; it += 2) {
+    if (it + 1 < ntiles) dma(K1, V1, it + 1);
+    run(K0, V0, it);
+    stage_sync();
+    if (it + 1 >= ntiles) break;
+    if (it + 2 < ntiles) dma(K0, V0, it + 2);
+    run(K1, V1, it + 1);
+    stage_sync();
   }
+
 
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {

@@ -124,6 +124,44 @@ MOBA_DEV u16x8_t ld_tr_operand(const uint16_t* X, int ld, int g16, int c0, int l
   return r;
 }
 
+// XOR-swizzled row-major LDS tiles of DP-element rows (no padding).  The
+// 16-byte block b of row r is stored at block b ^ f(r), f(r) = bitrev4(r % 16)
+// masked to the row's block count.  With 64 four-byte banks this keeps both
+// access patterns of the attention kernels conflict-free:
+//   * ds_read_b128 of one block from 16 consecutive rows (16 lanes per cycle);
+//   * ds_read_b64_tr_b16 of 4 consecutive rows x 4 consecutive blocks
+//     (32 lanes per cycle).
+template <int DP> MOBA_DEV int swz(int r, int col) {
+  constexpr int NBM = (DP / 8 < 16 ? DP / 8 : 16) - 1;
+  const int f = (int)(__builtin_bitreverse32((uint32_t)r) >> 28) & NBM;
+  return r * DP + ((((col >> 3) ^ f) << 3) | (col & 7));
+}
+
+// ld_tr_operand on a swizzled tile (same lane/key order).
+template <int DP>
+MOBA_DEV u16x8_t ld_tr_operand_swz(const uint16_t* X, int g16, int c0, int lane) {
+  const int hh = lane >> 5, sub = lane & 15, cb = c0 + ((lane >> 4) & 1) * 16;
+  const int r = g16 + 4 * hh + (sub >> 2), col = cb + 4 * (sub & 3);
+  const u16x4_t a = ld_tr4(X + swz<DP>(r, col)), b = ld_tr4(X + swz<DP>(r + 8, col));
+  u16x8_t o;
+  o[0] = a[0]; o[1] = a[1]; o[2] = a[2]; o[3] = a[3];
+  o[4] = b[0]; o[5] = b[1]; o[6] = b[2]; o[7] = b[3];
+  return o;
+}
+
+// Buffer resource over [base, base + bytes) for raw buffer loads (stride 0;
+// offsets at or past `bytes` read as zero).
+MOBA_DEV __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, bytes, 0x00020000);
+}
+
+// One 16-byte buffer load per lane straight into LDS: lane l's 16 bytes land
+// at lds + 16 * l (lds must be wave-uniform).
+MOBA_DEV void load_lds16(__amdgpu_buffer_rsrc_t r, uint16_t* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16,
+                                           voff, soff, 0, 0);
+}
+
 // 32-row query blocks per wave in the query-major attention kernels (forward
 // and dQ); a workgroup of 4 waves covers 128 * attn_qb rows.  One block per
 // wave leaves room for two waves per SIMD.
