@@ -83,10 +83,14 @@ __global__ __launch_bounds__(256) void delta_kernel(const uint16_t* __restrict__
 // operand; dQ^T = K^T dS^T reads K^T with the transposed LDS read.
 template <int DT, int DP, bool REMOTE, int QB>
 __global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a) {
-  constexpr int KS = DP + 8, NKS = DP / 16, NDB = DP / 32;
-  constexpr int NLD = kBN * DP / 8 / 256;
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kBN * KS];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][kBN * KS];
+  constexpr int NKS = DP / 16, NDB = DP / 32;
+  constexpr int TILE = kBN * DP, NB = DP / 8, NDMA = kBN * NB / 256;
+  // Two stages of K and V tiles (swz<DP> layout) filled by buffer loads
+  // straight into LDS, as in the forward kernel.
+  __shared__ __attribute__((aligned(16))) uint16_t K0[TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t V0[TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t K1[TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t V1[TILE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int qi = lane & 31, hh = lane >> 5;
@@ -150,26 +154,42 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a
     dl[qb] = valid[qb] ? a.delta[row] : 0.0f;
   }
 
-  u16x8_t kr[NLD], vr[NLD];
-  auto gload = [&](int kt0) {
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  uint32_t voff[NDMA];
+  bool vok[NDMA];
 #pragma unroll
-    for (int i = 0; i < NLD; ++i) {
-      const int id = tid + i * 256, key = id / (DP / 8), dc = (id % (DP / 8)) * 8;
-      const int kg = kt0 + key;
-      const bool ok = kg < k_hi && dc < D;
-      const int64_t off = ((int64_t)kg * a.Hkv + kh) * D + dc;
-      kr[i] = ok ? ld8(a.k + off) : zero8();
-      vr[i] = ok ? ld8(a.v + off) : zero8();
+  for (int n = 0; n < NDMA; ++n) {
+    const int j = (n * 4 + wave_s) * 64 + lane, row = j / NB;
+    const int col = swz<DP>(row, (j % NB) * 8) - row * DP;
+    voff[n] = (uint32_t)(((row * a.Hkv + kh) * D + col) * 2);
+    vok[n] = col < D;
+  }
+  const int n_keys = k_hi - k_lo;
+  const uint32_t nrec = (uint32_t)((((int64_t)(n_keys - 1) * a.Hkv + kh + 1) * D) * 2);
+  const uint16_t* kbase = a.k + (int64_t)k_lo * a.Hkv * D;
+  const uint16_t* vbase = a.v + (int64_t)k_lo * a.Hkv * D;
+  const uint32_t tile_bytes = (uint32_t)(kBN * a.Hkv * D * 2);
+  auto dma = [&](uint16_t* Kd, uint16_t* Vd, int it) {
+    const uint32_t soff = (uint32_t)it * tile_bytes;
+#pragma unroll
+    for (int n = 0; n < NDMA; ++n) {
+      if (vok[n]) {
+        load_lds16(make_rsrc(kbase, nrec), Kd + (n * 4 + wave_s) * 64 * 8, voff[n], soff);
+        load_lds16(make_rsrc(vbase, nrec), Vd + (n * 4 + wave_s) * 64 * 8, voff[n], soff);
+      }
     }
   };
-  auto lstore = [&](int buf) {
+  if (D < DP) {  // column blocks past D stay zero
 #pragma unroll
-    for (int i = 0; i < NLD; ++i) {
-      const int id = tid + i * 256, key = id / (DP / 8), dc = (id % (DP / 8)) * 8;
-      st8(&Ks[buf][key * KS + dc], kr[i]);
-      st8(&Vs[buf][key * KS + dc], vr[i]);
+    for (int n = 0; n < NDMA; ++n) {
+      const int j = (n * 4 + wave) * 64 + lane;
+      st8(K0 + j * 8, zero8()); st8(V0 + j * 8, zero8());
+      st8(K1 + j * 8, zero8()); st8(V1 + j * 8, zero8());
     }
-  };
+    __syncthreads();
+  }
+  const uint32_t kbase0 = swz_b128_base<DP>(lane);
+  const uint32_t trb0 = swz_tr_base<DP>(lane, 0), trb1 = swz_tr_base<DP>(lane, 1);
 
   f32x16_t acc[QB][NDB];
 #pragma unroll
@@ -178,14 +198,11 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a
     for (int db = 0; db < NDB; ++db) acc[qb][db] = zero16();
   const float c2 = a.scale_log2;
 
-  const int ntiles = (k_hi - k_lo + kBN - 1) / kBN;
-  gload(k_lo);
-  lstore(0);
-  __syncthreads();
-  for (int it = 0; it < ntiles; ++it) {
-    const int kt0 = k_lo + it * kBN, buf = it & 1;
-    if (it + 1 < ntiles) gload(kt0 + kBN);
-    const bool need_mask = (kt0 + kBN > k_hi) || (!REMOTE && kt0 + kBN - 1 > s_wave0);
+  const int ntiles = (n_keys + kBN - 1) / kBN;
+  auto tile = [&](const uint16_t* Kb, const uint16_t* Vb, const int it, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    const int kt0 = k_lo + it * kBN;
+    const uint32_t kq = opaque(kbase0), t0 = opaque(trb0), t1 = opaque(trb1);
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       f32x16_t sa[QB], pa[QB];
@@ -193,8 +210,8 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a
       for (int qb = 0; qb < QB; ++qb) { sa[qb] = zero16(); pa[qb] = zero16(); }
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {
-        const u16x8_t ka = ld8(&Ks[buf][(kb * 32 + qi) * KS + ks * 16 + hh * 8]);
-        const u16x8_t va = ld8(&Vs[buf][(kb * 32 + qi) * KS + ks * 16 + hh * 8]);
+        const uint32_t o = kb * 32 * DP * 2 + swz_b128<DP>(kq, ks);
+        const u16x8_t ka = lds8(Kb, o), va = lds8(Vb, o);
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
           sa[qb] = mfma32<DT>(ka, qf[qb][ks], sa[qb]);
@@ -209,7 +226,7 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           float p = fast_exp2(fmaf(sa[qb][r], c2, nl));
-          if (need_mask) {
+          if constexpr (MASK) {
             const int key = kt0 + kb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
             p = (key < k_hi && (REMOTE || key <= s[qb])) ? p : 0.0f;
           }
@@ -222,13 +239,52 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-          const u16x8_t kt = ld_tr_operand(Ks[buf], KS, kb * 32 + t * 16, db * 32, lane);
+          const uint32_t ro = (kb * 32 + t * 16) * DP * 2;
+          const u16x8_t kt = lds_tr8(Kb, ro + swz_tr<DP>(t0, db), ro + swz_tr<DP>(t1, db));
 #pragma unroll
           for (int qb = 0; qb < QB; ++qb) acc[qb][db] = mfma32<DT>(kt, dsv[qb][t], acc[qb][db]);
         }
+      // Issue order for this 32-key block: LDS operand reads run at most two
+      // MFMAs ahead, which bounds the registers they hold.
+      if constexpr (QB == 1) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+        for (int i = 0; i < NKS - 2; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 200, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+        for (int i = 0; i < 2 * NDB - 2; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (it + 1 < ntiles) lstore(buf ^ 1);
-    __syncthreads();
+  };
+  auto stage_sync = [&]() {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's tile loads landed
+    __builtin_amdgcn_s_barrier();
+  };
+  auto run = [&](const uint16_t* Kb, const uint16_t* Vb, int it) {
+    const int kt0 = k_lo + it * kBN;
+    const bool need_mask = (kt0 + kBN > k_hi) || (!REMOTE && kt0 + kBN - 1 > s_wave0);
+    if (need_mask) tile(Kb, Vb, it, std::true_type{}); else tile(Kb, Vb, it, std::false_type{});
+  };
+  dma(K0, V0, 0);
+  stage_sync();
+  for (int it = 0; it < ntiles; it += 2) {
+    if (it + 1 < ntiles) dma(K1, V1, it + 1);
+    run(K0, V0, it);
+    stage_sync();
+    if (it + 1 >= ntiles) break;
+    if (it + 2 < ntiles) dma(K0, V0, it + 2);
+    run(K1, V1, it + 1);
+    stage_sync();
   }
 
 #pragma unroll
@@ -308,12 +364,17 @@ template <int DP> constexpr int dkdv_qb() { return DP <= 128 ? 2 : 1; }
 template <int DT, int DP>
 __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
   constexpr int QB = dkdv_qb<DP>();
-  constexpr int QS = DP + 16, NKS = DP / 16, NDB = DP / 32;
+  constexpr int NKS = DP / 16, NDB = DP / 32;
   constexpr int BQ = 32 * QB;                 // query rows per tile
-  constexpr int NLD = (BQ * DP / 8 + 511) / 512;
+  constexpr int NB = DP / 8;                  // 16-byte blocks per row
+  constexpr int NDMA = (BQ * NB + 511) / 512; // blocks per thread per operand
   constexpr int WKEYS = kDkdvPairKeys;        // keys per wave pair
-  __shared__ __attribute__((aligned(16))) uint16_t Qs[2][BQ * QS];
-  __shared__ __attribute__((aligned(16))) uint16_t Gs[2][BQ * QS];
+  // Q / dO tiles in two named stages (swz<DP> layout), filled by buffer loads
+  // straight into LDS while the other stage is being used.
+  __shared__ __attribute__((aligned(16))) uint16_t Q0[BQ * DP];
+  __shared__ __attribute__((aligned(16))) uint16_t G0[BQ * DP];
+  __shared__ __attribute__((aligned(16))) uint16_t Q1[BQ * DP];
+  __shared__ __attribute__((aligned(16))) uint16_t G1[BQ * DP];
   __shared__ __attribute__((aligned(16))) float lse2s[2][BQ];
   __shared__ __attribute__((aligned(16))) float dels[2][BQ];
   __shared__ float Ps[4][QB][16][64];         // P handed from role P to role D
@@ -322,6 +383,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
   const int qi = lane & 31, hh = lane >> 5;
   const int pair = wave & 3;
   const bool role_p = wave < 4;
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   const int D = a.D, G = a.G;
   const int* tile = a.kv_tiles + 4 * blockIdx.x;
   const int c = tile[0], kt0 = tile[1], f = tile[2], kh = tile[3];
@@ -330,6 +392,18 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
   const int key0 = c_lo + kt0;              // first key of the workgroup
   const int wkey0 = key0 + pair * WKEYS;    // first key of this pair
   const int mykey = wkey0 + qi;             // this lane's key (B operand column)
+
+  // Uninitialised LDS could hold NaN patterns that a zero probability would
+  // not cancel; column blocks past D are never loaded and must read zero.
+#pragma unroll
+  for (int n = 0; n < NDMA; ++n) {
+    const int j = n * 512 + tid;
+    if (j < BQ * NB) {
+      st8(Q0 + j * 8, zero8()); st8(G0 + j * 8, zero8());
+      st8(Q1 + j * 8, zero8()); st8(G1 + j * 8, zero8());
+    }
+  }
+  __syncthreads();
 
   // The two roles run as separate instantiations of the body, so each wave's
   // code holds only its own role's registers.
@@ -369,61 +443,54 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
       return local < n_rem ? a.rows[rbase + local] >> 3 : -1;
     };
 
-    int nrow[NLD], nlrow = -1;
+    // Thread t loads blocks j = n * 512 + t of a tile: row j / NB, physical
+    // block j % NB, logical column block (j % NB) ^ f(row).
+    int nrow[NDMA], nlrow = -1;
     auto fetch_rows = [&](int it) {
 #pragma unroll
-      for (int i = 0; i < NLD; ++i) {
-        const int q = (tid + i * 512) / (DP / 8);
-        nrow[i] = q < BQ ? row_of(it, q) : -1;
+      for (int n = 0; n < NDMA; ++n) {
+        const int q = (n * 512 + tid) / NB;
+        nrow[n] = q < BQ ? row_of(it, q) : -1;
       }
       nlrow = tid < BQ ? row_of(it, tid) : -1;
     };
-    u16x8_t qr_[NLD], gr_[NLD];
-    float lse_r = INFINITY, del_r = 0.0f;
-    auto gload = [&]() {
+    const uint32_t qbytes = (uint32_t)((int64_t)a.T * a.Hq * D * 2);
+    auto dma = [&](uint16_t* Qd, uint16_t* Gd) {
 #pragma unroll
-      for (int i = 0; i < NLD; ++i) {
-        const int dc = ((tid + i * 512) % (DP / 8)) * 8;
-        const bool ok = nrow[i] >= 0 && dc < D;
-        qr_[i] = ok ? ld8(a.q + (int64_t)nrow[i] * D + dc) : zero8();
-        gr_[i] = ok ? ld8(a.dout + (int64_t)nrow[i] * D + dc) : zero8();
+      for (int n = 0; n < NDMA; ++n) {
+        const int j = n * 512 + tid, q = j / NB;
+        const int col = swz<DP>(q, (j % NB) * 8) - q * DP;
+        if (j < BQ * NB && col < D) {
+          // rows of -1 read past the end of the tensor: zeros
+          const uint32_t off = nrow[n] >= 0 ? (uint32_t)(((int64_t)nrow[n] * D + col) * 2) : qbytes;
+          const int jb = n * 512 + wave_s * 64;  // first block of this wave's 64
+          load_lds16(make_rsrc(a.q, qbytes), Qd + jb * 8, off, 0);
+          load_lds16(make_rsrc(a.dout, qbytes), Gd + jb * 8, off, 0);
+        }
       }
+    };
+    float lse_r = INFINITY, del_r = 0.0f;
+    auto load_ld = [&]() {
       lse_r = nlrow >= 0 ? a.lse[nlrow] * kLog2e : INFINITY;
       del_r = nlrow >= 0 ? a.delta[nlrow] : 0.0f;
     };
-    auto lstore = [&](int buf) {
-#pragma unroll
-      for (int i = 0; i < NLD; ++i) {
-        const int id = tid + i * 512, q = id / (DP / 8), dc = (id % (DP / 8)) * 8;
-        if (q < BQ) {
-          st8(&Qs[buf][q * QS + dc], qr_[i]);
-          st8(&Gs[buf][q * QS + dc], gr_[i]);
-        }
-      }
+    auto store_ld = [&](int buf) {
       if (tid < BQ) { lse2s[buf][tid] = lse_r; dels[buf][tid] = del_r; }
     };
 
+    const uint32_t kq0 = swz_b128_base<DP>(lane);
+    const uint32_t trb0 = swz_tr_base<DP>(lane, 0), trb1 = swz_tr_base<DP>(lane, 1);
     const float c2 = a.scale_log2;
-    if (it_lo < it_hi) {
-      fetch_rows(it_lo);
-      gload();
-      lstore(0);
-      fetch_rows(it_lo + 1);
-    }
-    __syncthreads();
-    for (int it = it_lo; it < it_hi; ++it) {
-      const int buf = (it - it_lo) & 1;
-      if (it + 1 < it_hi) {
-        gload();
-        fetch_rows(it + 2);
-      }
+
+    auto compute = [&](const uint16_t* Qb, const uint16_t* Gb, const int buf, const int it) {
+      const uint32_t kq = opaque(kq0), t0 = opaque(trb0), t1 = opaque(trb1);
       const bool is_self = it < G * n_self;
       const int sq0 = is_self ? self_begin + (it % n_self) * BQ : 0;
       // causal rows that end before the pair's first key contribute nothing
       const bool skip = is_self && sq0 + BQ - 1 < wkey0;
       const bool need_mask = (wkey0 + WKEYS > c_hi) || (is_self && sq0 < wkey0 + WKEYS - 1);
       // ---- first half: S -> P (role P) or dP (role D)
-      const uint16_t* A1 = ROLE_P ? Qs[buf] : Gs[buf];
+      const uint16_t* A1 = ROLE_P ? Qb : Gb;
       f32x16_t sp[QB];
       if (!skip) {
 #pragma unroll
@@ -432,7 +499,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
         for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
           for (int qb = 0; qb < QB; ++qb)
-            sp[qb] = mfma32<DT>(ld8(&A1[(qb * 32 + qi) * QS + ks * 16 + hh * 8]), kv[ks], sp[qb]);
+            sp[qb] = mfma32<DT>(lds8(A1, qb * 32 * DP * 2 + swz_b128<DP>(kq, ks)), kv[ks], sp[qb]);
         if constexpr (ROLE_P) {
           auto to_p = [&](auto mask_tag) {
             constexpr bool MASK = decltype(mask_tag)::value;
@@ -455,7 +522,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
           if (need_mask) to_p(std::true_type{}); else to_p(std::false_type{});
         }
       }
-      __syncthreads();
+      lds_barrier();
       // ---- second half: dV += P^T dO (role P) or dK += dS^T Q (role D)
       if (!skip) {
         u16x8_t op[QB][2];
@@ -479,18 +546,46 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
               }
             }
         }
-        const uint16_t* B2 = ROLE_P ? Gs[buf] : Qs[buf];
+        const uint16_t* B2 = ROLE_P ? Gb : Qb;
 #pragma unroll
         for (int i = 0; i < NDB; ++i)
 #pragma unroll
           for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
-              acc[i] = mfma32<DT>(op[qb][t], ld_tr_operand(B2, QS, qb * 32 + t * 16, i * 32, lane),
-                                  acc[i]);
+            for (int t = 0; t < 2; ++t) {
+              const uint32_t ro = (qb * 32 + t * 16) * DP * 2;
+              acc[i] = mfma32<DT>(op[qb][t],
+                                  lds_tr8(B2, ro + swz_tr<DP>(t0, i), ro + swz_tr<DP>(t1, i)), acc[i]);
+            }
       }
-      if (it + 1 < it_hi) lstore(buf ^ 1);
-      __syncthreads();
+    };
+
+    if (it_lo < it_hi) {
+      fetch_rows(it_lo);
+      load_ld();
+      dma(Q0, G0);
+      store_ld(0);
+      fetch_rows(it_lo + 1);
+    }
+    stage_barrier();
+    for (int it = it_lo; it < it_hi; it += 2) {
+      if (it + 1 < it_hi) {
+        load_ld();
+        dma(Q1, G1);
+        fetch_rows(it + 2);
+      }
+      compute(Q0, G0, 0, it);
+      if (it + 1 < it_hi) store_ld(1);
+      stage_barrier();
+      if (it + 1 >= it_hi) break;
+      if (it + 2 < it_hi) {
+        load_ld();
+        dma(Q0, G0);
+        fetch_rows(it + 3);
+      }
+      compute(Q1, G1, 1, it + 1);
+      if (it + 2 < it_hi) store_ld(0);
+      stage_barrier();
     }
 
     // D-layout: lane holds column d = i*32 + qi, keys 8j + 4hh + r.  With a
@@ -597,6 +692,7 @@ extern "C" int moba_hip_prefill_bwd(const void* q, const void* k, const void* v,
   if (Hq < 1 || Hkv < 1 || Hq % Hkv) { moba_set_error("prefill_bwd: Hq must be a positive multiple of Hkv"); return MOBA_ERR_ARG; }
   if (R < 0 || R > 8) { moba_set_error("prefill_bwd: remote count must be in [0,8]"); return MOBA_ERR_ARG; }
   if (parts < 1 || parts > 3) { moba_set_error("prefill_bwd: parts must be 1 (dq), 2 (dk/dv) or 3 (both)"); return MOBA_ERR_ARG; }
+  if ((int64_t)T * Hq * D * 2 >= ((int64_t)1 << 32)) { moba_set_error("prefill_bwd: q / dO must be smaller than 4 GiB (32-bit buffer offsets)"); return MOBA_ERR_ARG; }
   if (kv_splits < 1 || kv_splits > 16 || (kv_splits > 1 && (part_dkv == nullptr || D % 8))) { moba_set_error("prefill_bwd: kv_splits must be in [1,16], with a part_dkv workspace when > 1"); return MOBA_ERR_ARG; }
   BwdArgs a;
   a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v;

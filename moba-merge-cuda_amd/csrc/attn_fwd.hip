@@ -185,25 +185,15 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void fwd_kernel(FwdArgs 
   for (int qb = 0; qb < QB; ++qb) { m_run[qb] = -INFINITY; lsum[qb] = 0.0f; }
   const float c2 = a.scale_log2;
 
-  // Lane-constant swizzled LDS offsets (elements): the rows this lane reads
-  // differ from these by multiples of 16, which the swizzle ignores.
-  int kofs[NKS], vofs[NDB][2];
-#pragma unroll
-  for (int ks = 0; ks < NKS; ++ks) kofs[ks] = swz<DP>(qi, ks * 16 + hh * 8);
-  {
-    const int sub = lane & 15, r = 4 * hh + (sub >> 2);
-#pragma unroll
-    for (int db = 0; db < NDB; ++db) {
-      const int col = db * 32 + ((lane >> 4) & 1) * 16 + 4 * (sub & 3);
-      vofs[db][0] = swz<DP>(r, col);
-      vofs[db][1] = swz<DP>(r + 8, col);
-    }
-  }
+  // Lane-constant byte bases of the swizzled LDS reads.
+  const uint32_t kbase0 = swz_b128_base<DP>(lane);
+  const uint32_t trb0 = swz_tr_base<DP>(lane, 0), trb1 = swz_tr_base<DP>(lane, 1);
 
   const int ntiles = (n_keys + kBN - 1) / kBN;
   auto tile = [&](const uint16_t* Kb, const uint16_t* Vb, const int it, auto mask_tag) {
     constexpr bool MASK = decltype(mask_tag)::value;
     const int kt0 = k_lo + it * kBN;
+    const uint32_t kq = opaque(kbase0), t0 = opaque(trb0), t1 = opaque(trb1);
     f32x16_t sacc[QB][2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
@@ -211,7 +201,7 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void fwd_kernel(FwdArgs 
       for (int qb = 0; qb < QB; ++qb) sacc[qb][kb] = zero16();
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {
-        const u16x8_t av = ld8(Kb + kb * 32 * DP + kofs[ks]);
+        const u16x8_t av = lds8(Kb, kb * 32 * DP * 2 + swz_b128<DP>(kq, ks));
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) sacc[qb][kb] = mfma32<DT>(av, qf[qb][ks], sacc[qb][kb]);
       }
@@ -273,11 +263,8 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void fwd_kernel(FwdArgs 
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-          const uint16_t* vb = Vb + (kb * 32 + t * 16) * DP;
-          const u16x4_t x0 = ld_tr4(vb + vofs[db][0]), x1 = ld_tr4(vb + vofs[db][1]);
-          u16x8_t av;
-          av[0] = x0[0]; av[1] = x0[1]; av[2] = x0[2]; av[3] = x0[3];
-          av[4] = x1[0]; av[5] = x1[1]; av[6] = x1[2]; av[7] = x1[3];
+          const uint32_t ro = (kb * 32 + t * 16) * DP * 2;
+          const u16x8_t av = lds_tr8(Vb, ro + swz_tr<DP>(t0, db), ro + swz_tr<DP>(t1, db));
 #pragma unroll
           for (int qb = 0; qb < QB; ++qb) oacc[qb][db] = mfma32<DT>(av, pv[qb][kb][t], oacc[qb][db]);
         }

@@ -137,6 +137,51 @@ template <int DP> MOBA_DEV int swz(int r, int col) {
   return r * DP + ((((col >> 3) ^ f) << 3) | (col & 7));
 }
 
+// Byte-offset form of the swizzled reads.  The bank-spreading XOR f(r)
+// depends on r % 16 only, so a lane's rows (its own row plus multiples of 16)
+// share one lane-constant base.  A row starts at a multiple of 16 * NB bytes,
+// so adding block blk to a base is one XOR on the low block bits the swizzle
+// owns plus an add of the rest.
+template <int DP> constexpr int swz_nbm() { return (DP / 8 < 16 ? DP / 8 : 16) - 1; }
+template <int DP> MOBA_DEV uint32_t swz_add(uint32_t base, int blk) {
+  constexpr int NBM = swz_nbm<DP>();
+  return (base ^ (uint32_t)((blk & NBM) << 4)) + (uint32_t)((blk & ~NBM) << 4);
+}
+// ds_read_b128 operand of rows (lane % 32) + 16m, k-step ks: base for ks = 0.
+template <int DP> MOBA_DEV uint32_t swz_b128_base(int lane) {
+  return (uint32_t)swz<DP>(lane & 31, (lane >> 5) * 8) * 2;
+}
+template <int DP> MOBA_DEV uint32_t swz_b128(uint32_t base, int ks) { return swz_add<DP>(base, 2 * ks); }
+// Transposed-read pieces (rows g16 + 4hh + (l%16)/4 + 8*half, columns
+// 32*db + 16*((l/16)%2) + 4*(l%4)): base for g16 = 0, db = 0.
+template <int DP> MOBA_DEV uint32_t swz_tr_base(int lane, int half) {
+  const int sub = lane & 15;
+  return (uint32_t)swz<DP>(4 * (lane >> 5) + (sub >> 2) + 8 * half,
+                           ((lane >> 4) & 1) * 16 + 4 * (sub & 3)) * 2;
+}
+template <int DP> MOBA_DEV uint32_t swz_tr(uint32_t base, int db) { return swz_add<DP>(base, 4 * db); }
+
+// Hides a value from the optimiser so that addresses derived from it are
+// recomputed where they are used instead of being held in registers.
+MOBA_DEV uint32_t opaque(uint32_t x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+MOBA_DEV u16x8_t lds8(const uint16_t* base, uint32_t byte_off) {
+  return *reinterpret_cast<const u16x8_t*>(reinterpret_cast<const char*>(base) + byte_off);
+}
+// MFMA operand from two transposed reads at byte offsets a and b of base.
+MOBA_DEV u16x8_t lds_tr8(const uint16_t* base, uint32_t a, uint32_t b) {
+  const char* p = reinterpret_cast<const char*>(base);
+  const u16x4_t x = ld_tr4(reinterpret_cast<const uint16_t*>(p + a));
+  const u16x4_t y = ld_tr4(reinterpret_cast<const uint16_t*>(p + b));
+  u16x8_t o;
+  o[0] = x[0]; o[1] = x[1]; o[2] = x[2]; o[3] = x[3];
+  o[4] = y[0]; o[5] = y[1]; o[6] = y[2]; o[7] = y[3];
+  return o;
+}
+
 // ld_tr_operand on a swizzled tile (same lane/key order).
 template <int DP>
 MOBA_DEV u16x8_t ld_tr_operand_swz(const uint16_t* X, int g16, int c0, int lane) {
@@ -160,6 +205,26 @@ MOBA_DEV __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
 MOBA_DEV void load_lds16(__amdgpu_buffer_rsrc_t r, uint16_t* lds, uint32_t voff, uint32_t soff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16,
                                            voff, soff, 0, 0);
+}
+
+// Workgroup barriers for kernels whose LDS tiles arrive by buffer loads.
+// The empty asm statements keep the compiler from moving memory accesses
+// across the barrier; the explicit waits are visible to its wait-count pass.
+//   stage_barrier: this wave's buffer loads (and LDS accesses) complete, then
+//                  the barrier: every wave's loads have landed after it.
+//   lds_barrier:   LDS accesses complete, then the barrier; buffer loads in
+//                  flight stay in flight.
+MOBA_DEV void stage_barrier() {
+  __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+MOBA_DEV void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 // 32-row query blocks per wave in the query-major attention kernels (forward
