@@ -94,8 +94,10 @@ int moba_hip_prefill_fwd(const void* q, const void* k, const void* v, int dtype,
  * packed remote grads (grouped_attention.py:81-89).  out/dout [T,Hq,D],
  * lse [T,Hq] from the forward; kv_tiles[n_kv_tiles][4] = (chunk, first key,
  * filtered index or -1, kv head): one workgroup per entry, tiles of 128
- * keys; chunk -1 marks an empty entry.  delta [T*Hq] and
- * part_dq [T*Hq*R, D] fp32 are workspaces.  dq [T,Hq,D], dk/dv [T,Hkv,D]
+ * keys; chunk -1 marks an empty entry.  delta [2*T*Hq] and
+ * part_dq [T*Hq*R, D] fp32 are workspaces.  pack is a workspace of
+ * T*Hq*R*(4*D + 8) bytes for parts & 2 when R > 0 and D <= 64 (the expert
+ * rows of q, dO, lse and delta copied contiguously), else may be NULL.  dq [T,Hq,D], dk/dv [T,Hkv,D]
  * (dtype) are fully written (every key belongs to exactly one kv tile).
  * parts selects the launches: 1 = Delta and dq (query-major kernels), 2 = dk/dv
  * (key-major kernel, needs the Delta of a parts-1 call), 3 = both in order.
@@ -110,7 +112,8 @@ int moba_hip_prefill_bwd(const void* q, const void* k, const void* v, const void
                          int R, const int* filtered, int E, const int* tile_off,
                          const int* row_off, const int* counts, const int* rows,
                          int max_remote_tiles, float* delta, float* part_dq, void* dq, void* dk,
-                         void* dv, int parts, int kv_splits, float* part_dkv, void* stream);
+                         void* dv, int parts, int kv_splits, float* part_dkv, void* pack,
+                         void* stream);
 
 /* ----------------------------------------------------------------- decode */
 

@@ -38,10 +38,22 @@ def _headers():
     return max((h.stat().st_mtime for h in hs), default=0.0)
 
 
+# Per-source flag changes.  attn_dkdv.hip runs one wave per SIMD: its dK / dV
+# accumulators belong in AGPRs, so it is built without the VGPR-form flag.
+NO_VGPR_FORM = {"attn_dkdv.hip"}
+
+
+def _flags(src: Path):
+    if src.name in NO_VGPR_FORM:
+        i = FLAGS.index("-amdgpu-mfma-vgpr-form")
+        return FLAGS[:i - 1] + FLAGS[i + 1:]
+    return FLAGS
+
+
 def _compile(src: Path, force: bool) -> Path:
     obj = OUT_DIR / (src.stem + ".o")
     if force or not obj.exists() or obj.stat().st_mtime < max(src.stat().st_mtime, _headers()):
-        cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
+        cmd = [HIPCC, *_flags(src), "-c", str(src), "-o", str(obj)]
         r = subprocess.run(cmd, capture_output=True, text=True)
         if r.returncode:
             sys.stderr.write(r.stdout + r.stderr)

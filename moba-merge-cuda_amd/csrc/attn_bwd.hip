@@ -20,48 +20,23 @@
 #include <type_traits>
 
 #include "common.h"
+#include "bwd_args.h"
 #include "../../include/moba_hip.h"
 
 using namespace moba;
 
 namespace {
 
-struct BwdArgs {
-  const uint16_t* q;
-  const uint16_t* k;
-  const uint16_t* v;
-  const uint16_t* out;
-  const uint16_t* dout;
-  const float* lse;
-  int T, Hq, Hkv, D, G;
-  float scale, scale_log2;
-  const int* cu_chunk;
-  const int* self_tiles;
-  const int* kv_tiles;
-  const int* sel;
-  int R;
-  const int* filtered;
-  int E;
-  const int* tile_off;
-  const int* row_off;
-  const int* counts;
-  const int* rows;
-  float* delta;
-  float* part_dq;
-  float* part_dkv;   // [kv_splits][2][T, Hkv, D] fp32 when kv_splits > 1
-  int kv_splits;
-  uint16_t* dq;
-  uint16_t* dk;
-  uint16_t* dv;
-};
 
 constexpr int kBN = 64;   // dq: keys per LDS tile
 
 // ------------------------------------------------------------------ delta
 template <int DT>
 __global__ __launch_bounds__(256) void delta_kernel(const uint16_t* __restrict__ o,
-                                                    const uint16_t* __restrict__ g, int64_t rows,
-                                                    int D, float* __restrict__ delta) {
+                                                    const uint16_t* __restrict__ g,
+                                                    const float* __restrict__ lse, int64_t rows,
+                                                    int D, float* __restrict__ delta,
+                                                    float* __restrict__ lse2) {
   const int sub = threadIdx.x & 15;
   const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
   float acc = 0.0f;
@@ -74,7 +49,30 @@ __global__ __launch_bounds__(256) void delta_kernel(const uint16_t* __restrict__
   }
 #pragma unroll
   for (int off = 8; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 16);
-  if (row < rows && sub == 0) delta[row] = acc;
+  if (row < rows && sub == 0) {
+    delta[row] = acc;
+    lse2[row] = lse[row] * kLog2e;
+  }
+}
+
+// ------------------------------------------------------------------- pack
+// Copies the expert rows (rows[m] >> 3 for m < row_off[E]) of q, dO, lse2 and
+// delta into contiguous packed arrays, so that the key-major kernel reads
+// every query tile with affine addresses.  One 16-byte piece per thread.
+__global__ __launch_bounds__(256) void pack_rows_kernel(BwdArgs a) {
+  const int nb = a.D / 8;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t m = i / nb;
+  const int M = a.row_off[a.E];
+  if (m >= M) return;
+  const int b = (int)(i % nb);
+  const int64_t row = a.rows[m] >> 3;
+  st8(a.pack_q + m * a.D + b * 8, ld8(a.q + row * a.D + b * 8));
+  st8(a.pack_g + m * a.D + b * 8, ld8(a.dout + row * a.D + b * 8));
+  if (b == 0) {
+    a.pack_lse2[m] = a.lse2[row];
+    a.pack_delta[m] = a.delta[row];
+  }
 }
 
 // --------------------------------------------------------------------- dq
@@ -650,15 +648,23 @@ int launch_bwd(const BwdArgs& a, int n_self, int n_kv, int max_remote, int parts
   const int64_t rows = (int64_t)a.T * a.Hq;
   if (parts & 1) {
     hipLaunchKernelGGL(delta_kernel<DT>, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, st,
-                       a.out, a.dout, rows, a.D, a.delta);
+                       a.out, a.dout, a.lse, rows, a.D, a.delta, a.lse2);
     if (max_remote > 0 && a.R > 0)
       hipLaunchKernelGGL((dq_kernel<DT, DP, true, attn_qb<DP>()>), dim3((max_remote + 7) / 8 * 8), dim3(256), 0, st, a);
     if (n_self > 0)
       hipLaunchKernelGGL((dq_kernel<DT, DP, false, attn_qb<DP>()>), dim3(n_self, a.Hq), dim3(256), 0, st, a);
   }
   if ((parts & 2) && n_kv > 0) {
-    // 4 wave pairs x kDkdvPairKeys keys per workgroup; the host's key tiles match
-    hipLaunchKernelGGL((dkdv_kernel<DT, DP>), dim3(n_kv, a.kv_splits), dim3(512), 0, st, a);
+    // 128 keys per workgroup in both kernels; the host's key tiles match
+    if constexpr (DP <= 64) {
+      if (a.pack_rows > 0) {
+        const int64_t pieces = a.pack_rows * (a.D / 8);
+        hipLaunchKernelGGL(pack_rows_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, st, a);
+      }
+      launch_dkdv1<DT, DP>(a, n_kv, st);
+    } else {
+      hipLaunchKernelGGL((dkdv_kernel<DT, DP>), dim3(n_kv, a.kv_splits), dim3(512), 0, st, a);
+    }
     if (a.kv_splits > 1) {
       const int64_t n4 = (int64_t)a.T * a.Hkv * a.D / 4;
       hipLaunchKernelGGL(dkdv_reduce_kernel<DT>, dim3((unsigned)((2 * n4 + 255) / 256)), dim3(256), 0,
@@ -686,7 +692,8 @@ extern "C" int moba_hip_prefill_bwd(const void* q, const void* k, const void* v,
                                     int E, const int* tile_off, const int* row_off,
                                     const int* counts, const int* rows, int max_remote_tiles,
                                     float* delta, float* part_dq, void* dq, void* dk, void* dv,
-                                    int parts, int kv_splits, float* part_dkv, void* stream) {
+                                    int parts, int kv_splits, float* part_dkv, void* pack,
+                                    void* stream) {
   if (dtype != 0 && dtype != 1) { moba_set_error("prefill_bwd: dtype must be 0 (bf16) or 1 (fp16)"); return MOBA_ERR_ARG; }
   if (D < 8 || D > 256 || D % 8) { moba_set_error("prefill_bwd: head_dim must be a multiple of 8 in [8,256]"); return MOBA_ERR_ARG; }
   if (Hq < 1 || Hkv < 1 || Hq % Hkv) { moba_set_error("prefill_bwd: Hq must be a positive multiple of Hkv"); return MOBA_ERR_ARG; }
@@ -704,6 +711,14 @@ extern "C" int moba_hip_prefill_bwd(const void* q, const void* k, const void* v,
   a.tile_off = tile_off; a.row_off = row_off; a.counts = counts; a.rows = rows;
   a.delta = delta; a.part_dq = part_dq; a.part_dkv = part_dkv; a.kv_splits = kv_splits;
   a.dq = (uint16_t*)dq; a.dk = (uint16_t*)dk; a.dv = (uint16_t*)dv;
+  a.lse2 = delta + (int64_t)T * Hq;
+  a.pack_rows = (R > 0 && D <= 64) ? (int64_t)T * Hq * R : 0;
+  a.pack_q = (uint16_t*)pack;
+  a.pack_g = a.pack_q + a.pack_rows * D;
+  a.pack_lse2 = (float*)(a.pack_g + a.pack_rows * D);
+  a.pack_delta = a.pack_lse2 + a.pack_rows;
+  if (a.pack_rows > 0 && (parts & 2) && pack == nullptr) { moba_set_error("prefill_bwd: the pack workspace is required when R > 0 and head_dim <= 64"); return MOBA_ERR_ARG; }
+  if (a.pack_rows * D * 2 >= ((int64_t)1 << 32)) { moba_set_error("prefill_bwd: packed expert rows must be smaller than 4 GiB (32-bit buffer offsets)"); return MOBA_ERR_ARG; }
   hipStream_t st = (hipStream_t)stream;
   const int mr = R > 0 ? max_remote_tiles : 0;
   return dtype == 0 ? dispatch_bwd<0>(a, n_self_tiles, n_kv_tiles, mr, parts, st)

@@ -27,7 +27,7 @@ SIGNATURES = {
                              _P, _P, _P, _P, _I, _P, _P, _P, _P, _P],
     "moba_hip_prefill_bwd": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _I, _P, _I,
                              _P, _I, _P, _I, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _I, _P,
-                             _P],
+                             _P, _P],
     "moba_hip_decode_work_items": [_I, _I, _I],
     "moba_hip_paged_append": [_P, _P, _I, _I, _I, _I, _P, _P, _I, _P, _I, _P, _P, _P],
     "moba_hip_block_means": [_P, _I, _I, _I, _I, _P, _I, _P, _P, _I, _I, _I, _P, _I, _P],

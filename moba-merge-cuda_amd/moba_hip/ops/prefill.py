@@ -220,7 +220,7 @@ def backward(plan: PrefillPlan, q, k, v, out, lse, dout, rt: RouteResult | None)
     dev = q.device
     R = plan.remote
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    delta = torch.empty(T * hq, dtype=torch.float32, device=dev)
+    delta = torch.empty(2 * T * hq, dtype=torch.float32, device=dev)
     part_dq = torch.empty((T * hq * R, d), dtype=torch.float32, device=dev) if R else None
     args = [q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
             dout.data_ptr(), lse.data_ptr(), DTYPE_CODE[q.dtype], T, hq, plan.hkv, d,
@@ -234,12 +234,15 @@ def backward(plan: PrefillPlan, q, k, v, out, lse, dout, rt: RouteResult | None)
     ks = plan.kv_splits
     part_dkv = (torch.empty(ks * 2 * T * plan.hkv * d, dtype=torch.float32, device=dev)
                 if ks > 1 else None)
+    # expert rows of q / dO / lse / delta packed contiguously for the key-major kernel
+    pack = (torch.empty(T * hq * R * (4 * d + 8), dtype=torch.uint8, device=dev)
+            if R and d <= 64 else None)
     st = _lib.stream_of(dev)
-    _lib.call("moba_hip_prefill_bwd", *args, 1, ks, _lib.ptr(part_dkv), st)
+    _lib.call("moba_hip_prefill_bwd", *args, 1, ks, _lib.ptr(part_dkv), None, st)
     events = DKDV_EVENTS
     if events is not None:
         events[0].record()
-    _lib.call("moba_hip_prefill_bwd", *args, 2, ks, _lib.ptr(part_dkv), st)
+    _lib.call("moba_hip_prefill_bwd", *args, 2, ks, _lib.ptr(part_dkv), _lib.ptr(pack), st)
     if events is not None:
         events[1].record()
     return dq, dk, dv

@@ -105,11 +105,11 @@ def test_argument_errors_are_reported_without_a_device():
     with pytest.raises(_lib.MobaHipError, match="head_dim"):
         _lib.call("moba_hip_prefill_bwd", None, None, None, None, None, None, 0, 1, 1, 1, 12,
                   1.0, None, None, 0, None, 0, None, 0, None, 0, None, None, None, None, 0,
-                  None, None, None, None, None, 3, 1, None, None)
+                  None, None, None, None, None, 3, 1, None, None, None)
     with pytest.raises(_lib.MobaHipError, match="kv_splits"):
         _lib.call("moba_hip_prefill_bwd", None, None, None, None, None, None, 0, 1, 1, 1, 64,
                   1.0, None, None, 0, None, 0, None, 0, None, 0, None, None, None, None, 0,
-                  None, None, None, None, None, 3, 2, None, None)
+                  None, None, None, None, None, 3, 2, None, None, None)
     with pytest.raises(_lib.MobaHipError, match="remote count"):
         _lib.call("moba_hip_route_prefill", None, 0, 1, 1, 1, 8, None, None, 1, None, None, 9, 1,
                   None, None, None)
