@@ -198,11 +198,12 @@ int moba_hip_decode_step(int* table, int table_width, int* lengths, const int* i
  * a route width whose scratch fits LDS. */
 int moba_hip_decode_fused_supported(int Hq, int Hkv, int D, int width, int table_width);
 
-/* Whole decode for Nq query rows (one query per row) in ONE launch:
- * routing (scores over the closed chunks c < min(pos / chunk, width), stable
- * top-R per q head, selected [Nq,Hq,R+1] with slot 0 = pos / chunk, -1 pad;
- * not written when dense), the paged attention over the union of the heads'
- * chunks, out [Nq,Hq,D] and lse [Nq,Hq] fp32 natural log.
+/* Whole decode for Nq query rows (one query per row), two launches on the
+ * stream: routing (scores over the closed chunks c < min(pos / chunk, width),
+ * stable top-R per q head, selected [Nq,Hq,R+1] with slot 0 = pos / chunk, -1
+ * pad; not written when dense) and the paged attention over the union of the
+ * heads' chunks into S split partials, then their merge into out [Nq,Hq,D]
+ * and lse [Nq,Hq] fp32 natural log.
  * pos_mode 0: positions [Nq] are given (read only; no table, length or pool
  *             change).
  * pos_mode 1: position = lengths[ids[row]] - 1 (prepared attend); the
@@ -213,10 +214,8 @@ int moba_hip_decode_fused_supported(int Hq, int Hkv, int D, int width, int table
  *             the chunk it closes is written to means (canonical order, as
  *             moba_hip_block_means), and lengths advance by one.
  * splits S in [1,64] workgroups per (row, kv head); workspaces part_o
- * [Nq*Hq*S, D] and part_ml [Nq*Hq*S, 2] fp32; counters [Nq*Hkv + Nq] int32
- * must be zero before the first launch and are left zero by every launch.
- * width must be >= max(position) / chunk.  Launches on one counters buffer
- * must not overlap.  Outputs are deterministic for a fixed S.
+ * [Nq*Hq*S, D] and part_ml [Nq*Hq*S, 2] fp32.  width must be >=
+ * max(position) / chunk.  Outputs are deterministic for a fixed S.
  * Replaces _metadata + _append_kernel + _step_means + _route_kernel + top-k +
  * _selected + _attention_kernel (prepared_decode.py:6-94, paged_decode.py:10-112). */
 int moba_hip_decode_fused(const void* q, const void* k, const void* v, int dtype, int Nq, int Hq,
@@ -224,8 +223,7 @@ int moba_hip_decode_fused(const void* q, const void* k, const void* v, int dtype
                           int table_width, int* lengths, const int* ids, int* positions,
                           const int* delta, void* means, int max_chunks, int chunk, int width,
                           int R, int dense, int pos_mode, int splits, int* selected,
-                          float* part_o, float* part_ml, int* counters, void* out, float* lse,
-                          void* stream);
+                          float* part_o, float* part_ml, void* out, float* lse, void* stream);
 
 #ifdef __cplusplus
 }

@@ -7,24 +7,25 @@
 // (_step_means), route scores + stable top-k + selected slots (_route_kernel,
 // _stable_topk, _selected) and the attention (_attention_kernel).
 //
-// Grid: (splits S, query rows x kv heads).  Every workgroup of a (query, kv
-// head) first recomputes the route of the group's G <= 16 q heads (the work
-// is tiny: G x closed chunks dot products against the stored means), giving
-// every workgroup the same union of selected chunks.  The union's tokens, cut
-// into 32-token blocks, are split evenly over the S workgroups; each
-// workgroup's 4 waves take its blocks round-robin: S^T = K Q^T on
-// v_mfma_f32_16x16x32 (16 tokens x the 16 heads, K straight from the page
-// pool, heads that did not select the block's chunk masked), O^T += V^T P^T
-// with V^T from a wave-private LDS tile by the transposed read.  The waves
-// merge in LDS into one (o, max, sum) partial per (head, split).  The last
-// workgroup of the (query, kv head) to arrive (device-scope counter) merges
-// the S partials in split order, so the result does not depend on arrival
-// order, and resets the counter for the next launch.
+// Two launches.  fused_kernel, grid (splits S, query rows x kv heads): every
+// workgroup of a (query, kv head) first recomputes the route of the group's
+// G <= 16 q heads (the work is tiny: G x closed chunks dot products against
+// the stored means), giving every workgroup the same union of selected
+// chunks.  The union's tokens, cut into 32-token blocks, are split evenly over
+// the S workgroups; each workgroup's 4 waves take its blocks round-robin:
+// S^T = K Q^T on v_mfma_f32_16x16x32 (16 tokens x the 16 heads, K straight
+// from the page pool, heads that did not select the block's chunk masked),
+// O^T += V^T P^T with V^T from a wave-private LDS tile by the transposed read.
+// The waves merge in LDS into one (o, max, sum) partial per (head, split).
+// merge_kernel, one wave per (query, q head), then combines the S partials in
+// split order (deterministic for a fixed S).  The launch boundary orders the
+// partial stores before the merge reads, with no device-scope fences or
+// arrival counters inside either kernel.
 //
 // Step mode: the new token's K/V are read from the input rows (so no
 // workgroup waits for the scatter); split 0 scatters them and applies the
 // page-table delta, the last split computes the closing chunk mean, and the
-// last workgroup of the query row advances its length.
+// merge advances the row's position and length.
 #include "common.h"
 #include "../../include/moba_hip.h"
 
@@ -53,7 +54,6 @@ struct FusedArgs {
   int* selected;       // [Nq, Hq, R + 1] or null
   float* part_o;       // [Nq, Hq, S, D]
   float* part_ml;      // [Nq, Hq, S, 2]
-  int* counters;       // [Nq * Hkv + Nq], zero between launches
   uint16_t* out;       // [Nq, Hq, D]
   float* lse;          // [Nq, Hq]
 };
@@ -517,77 +517,59 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
     a.part_o[entry * D + d] = z > 0.0f ? acc / z : 0.0f;
     if (d == 0) { a.part_ml[2 * entry] = M; a.part_ml[2 * entry + 1] = z; }
   }
+}
 
-  // ---- the last workgroup of this (query, kv head) merges the splits.  The
-  // barrier completes every thread's partial stores; one agent-scope release
-  // by thread 0 then publishes them (L2 writeback) before the arrival count,
-  // and the last arrival's agent-scope acquire makes all splits visible.
-  __syncthreads();
-  if (tid == 0) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    const bool last = atomicAdd(&a.counters[rowk], 1) == S - 1;
-    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    s_info[6] = last;
+// Combines the S split partials of one (query, q head): weights
+// w_s = z_s 2^(m_s - M), O = sum w_s o_s / sum w_s, LSE = M + log2(sum w_s)
+// (natural log on output), summed in split order.  In prepared modes the
+// wave of head 0 also publishes the row's position (and, in step mode,
+// advances its length): every attention workgroup has read it by now.
+template <int DT>
+__global__ __launch_bounds__(64) void merge_kernel(FusedArgs a, int S) {
+  const int lane = threadIdx.x;
+  const int rh = blockIdx.x, qrow = rh / a.Hq, h = rh % a.Hq;
+  const int sid = a.ids[qrow];
+  int p;
+  if (a.pos_mode == 0) {
+    p = a.positions[qrow];
+  } else {
+    const int len = a.lengths[sid];
+    p = a.pos_mode == 2 ? len : len - 1;
   }
-  __syncthreads();
-  if (!s_info[6]) return;
-  // split weights in LDS: w[g][s] = z_s * 2^(m_s - M_g), one parallel load round
-  float* wts = reinterpret_cast<float*>(lds);   // [16][S]
-  float* gM = wts + 16 * S;                     // [16]
-  float* gZ = gM + 16;                          // [16]
-  for (int x = tid; x < G * S; x += 64 * kFW) {
-    const int64_t e = ((int64_t)qrow * a.Hq + kh * G + x / S) * S + x % S;
-    const float m = a.part_ml[2 * e], z = a.part_ml[2 * e + 1];
-    wts[x] = z > 0.0f ? m : -INFINITY;
-    wts[16 * S + 32 + x] = z;  // staged sums
-  }
-  __syncthreads();
-  if (tid < G) {
-    float M = -INFINITY;
-    for (int s = 0; s < S; ++s) M = fmaxf(M, wts[tid * S + s]);
-    float Z = 0.0f;
-    for (int s = 0; s < S; ++s) {
-      const float z = wts[16 * S + 32 + tid * S + s];
-      const float wgt = z > 0.0f ? z * fast_exp2(wts[tid * S + s] - M) : 0.0f;
-      wts[tid * S + s] = wgt;
-      Z += wgt;
-    }
-    gM[tid] = M;
-    gZ[tid] = Z;
-  }
-  __syncthreads();
-  // 4 consecutive d per thread: 16-byte loads, up to 16 splits in flight
-  const int D4 = D / 4;
-  for (int x = tid; x < G * D4; x += 64 * kFW) {
-    const int g = x / D4, d = (x % D4) * 4;
-    const int64_t row = (int64_t)qrow * a.Hq + kh * G + g;
-    const f32x4_t* po = reinterpret_cast<const f32x4_t*>(a.part_o + row * S * D + d);
-    const float* wg = wts + g * S;
+  if (p < 0 || p / a.C > a.width) return;  // the attention launch skipped this row
+  const int64_t e0 = (int64_t)rh * S;
+  const float m = lane < S ? a.part_ml[2 * (e0 + lane)] : -INFINITY;
+  const float z = lane < S ? a.part_ml[2 * (e0 + lane) + 1] : 0.0f;
+  const float M = wave_max(z > 0.0f ? m : -INFINITY);
+  const float wgt = z > 0.0f ? z * fast_exp2(m - M) : 0.0f;
+  __shared__ float ws[64];
+  ws[lane] = wgt;
+  __builtin_amdgcn_wave_barrier();
+  // Z in split order (a fixed-order sum, not a tree)
+  float Z = 0.0f;
+  for (int s = 0; s < S; ++s) Z += ws[s];
+  const int d = lane * 4;
+  if (d < a.D) {
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    const f32x4_t* po = reinterpret_cast<const f32x4_t*>(a.part_o + e0 * a.D + d);
 #pragma unroll 16
     for (int s = 0; s < S; ++s) {
-      const f32x4_t o = po[(int64_t)s * D4];
-      const float wv = wg[s];
+      const f32x4_t o = po[(int64_t)s * (a.D / 4)];
+      const float wv = ws[s];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc[e] += wv * o[e];
+      for (int i = 0; i < 4; ++i) acc[i] += wv * o[i];
     }
-    const float iz = 1.0f / gZ[g];
+    const float iz = Z > 0.0f ? 1.0f / Z : 0.0f;
     u16x4_t r;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) r[e] = from_f32<DT>(acc[e] * iz);
-    *reinterpret_cast<u16x4_t*>(a.out + row * D + d) = r;
-    if (d == 0) a.lse[row] = (gM[g] + log2f(gZ[g])) * kLn2;
+    for (int i = 0; i < 4; ++i) r[i] = from_f32<DT>(acc[i] * iz);
+    *reinterpret_cast<u16x4_t*>(a.out + (int64_t)rh * a.D + d) = r;
   }
-  if (tid == 0) {
-    a.counters[rowk] = 0;
-    if (a.pos_mode != 0) {
-      // the row's last kv head finished: publish its position and advance its length
-      const int done = atomicAdd(&a.counters[a.Nq * a.Hkv + qrow], 1);
-      if (done == a.Hkv - 1) {
-        a.counters[a.Nq * a.Hkv + qrow] = 0;
-        a.positions[qrow] = p;
-        if (step) a.lengths[sid] = p + 1;
-      }
+  if (lane == 0) {
+    a.lse[rh] = (M + log2f(Z)) * kLn2;
+    if (a.pos_mode != 0 && h == 0) {
+      a.positions[qrow] = p;
+      if (a.pos_mode == 2) a.lengths[sid] = p + 1;
     }
   }
 }
@@ -596,6 +578,7 @@ template <int DT, int DP>
 int launch_fused(const FusedArgs& a, int splits, size_t dyn, hipStream_t st) {
   dim3 grid((unsigned)splits, (unsigned)(a.Nq * a.Hkv));
   hipLaunchKernelGGL((fused_kernel<DT, DP>), grid, dim3(64 * kFW), dyn, st, a);
+  hipLaunchKernelGGL((merge_kernel<DT>), dim3((unsigned)(a.Nq * a.Hq)), dim3(64), 0, st, a, splits);
   return moba_launch_status("decode_fused");
 }
 
@@ -621,7 +604,7 @@ extern "C" int moba_hip_decode_fused(const void* q, const void* k, const void* v
                                      const int* ids, int* positions, const int* delta, void* means,
                                      int max_chunks, int chunk, int width, int R, int dense,
                                      int pos_mode, int splits, int* selected, float* part_o,
-                                     float* part_ml, int* counters, void* out, float* lse,
+                                     float* part_ml, void* out, float* lse,
                                      void* stream) {
   if (dtype != 0 && dtype != 1) { moba_set_error("decode_fused: dtype must be 0 (bf16) or 1 (fp16)"); return MOBA_ERR_ARG; }
   if (!moba_hip_decode_fused_supported(Hq, Hkv, D, width, table_width)) {
@@ -642,7 +625,7 @@ extern "C" int moba_hip_decode_fused(const void* q, const void* k, const void* v
   a.scale_log2 = kLog2e / sqrtf((float)D);
   a.table = table; a.lengths = lengths; a.ids = ids; a.positions = positions; a.delta = delta;
   a.means = (uint16_t*)means; a.selected = selected; a.part_o = part_o; a.part_ml = part_ml;
-  a.counters = counters; a.out = (uint16_t*)out; a.lse = lse;
+  a.out = (uint16_t*)out; a.lse = lse;
   const size_t dyn = fused_route_lds(a.G, width);
   hipStream_t st = (hipStream_t)stream;
   return dtype == 0 ? dispatch_fused<0>(a, splits, dyn, st) : dispatch_fused<1>(a, splits, dyn, st);

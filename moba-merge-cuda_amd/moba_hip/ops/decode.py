@@ -93,16 +93,14 @@ def fused_splits(nq, hkv) -> int:
 
 
 class FusedWork:
-    """Persistent workspaces of ``fused``: split partials and arrival counters
-    (zeroed once; every launch leaves them zero)."""
-    __slots__ = ("splits", "part_o", "part_ml", "counters")
+    """Persistent workspaces of ``fused``: the split partials."""
+    __slots__ = ("splits", "part_o", "part_ml")
 
     def __init__(self, nq, hq, hkv, d, device, splits=None):
         self.splits = splits or fused_splits(nq, hkv)
         n = nq * hq * self.splits
         self.part_o = torch.empty((n, d), dtype=torch.float32, device=device)
         self.part_ml = torch.empty((n, 2), dtype=torch.float32, device=device)
-        self.counters = torch.zeros(nq * hkv + nq, dtype=torch.int32, device=device)
 
 
 def fused_args(q, k, v, kc, vc, table, lengths, ids, positions, delta, means, chunk, width,
@@ -115,7 +113,7 @@ def fused_args(q, k, v, kc, vc, table, lengths, ids, positions, delta, means, ch
             lengths.data_ptr(), ids.data_ptr(), positions.data_ptr(), _lib.ptr(delta),
             means.data_ptr(), means.shape[1], chunk, width, remote, 1 if dense else 0, pos_mode,
             work.splits, _lib.ptr(selected), work.part_o.data_ptr(), work.part_ml.data_ptr(),
-            work.counters.data_ptr(), out.data_ptr(), lse.data_ptr())
+            out.data_ptr(), lse.data_ptr())
 
 
 def launch_fused(args, stream):
