@@ -213,17 +213,22 @@ int moba_hip_decode_fused_supported(int Hq, int Hkv, int D, int width, int table
  *             new token k/v [Nq,Hkv,D] is scattered into the pool, the mean of
  *             the chunk it closes is written to means (canonical order, as
  *             moba_hip_block_means), and lengths advance by one.
- * splits S in [1,64] workgroups per (row, kv head); workspaces part_o
- * [Nq*Hq*S, D] and part_ml [Nq*Hq*S, 2] fp32.  width must be >=
- * max(position) / chunk.  Outputs are deterministic for a fixed S.
+ * splits S in [1,64] workgroups per (row, kv head), or, with a schedule
+ * sched (may be null), at most S: sched holds n_sched workgroup entries
+ * (row * Hkv + kv head, split, splits of that row), every split of every
+ * (row, kv head) exactly once, followed by the Nq*Hkv split counts.
+ * Workspaces part_o [Nq*Hq*S, D] and part_ml [Nq*Hq*S, 2] fp32.  width must
+ * be >= max(position) / chunk.  Outputs are deterministic for a fixed
+ * schedule.
  * Replaces _metadata + _append_kernel + _step_means + _route_kernel + top-k +
  * _selected + _attention_kernel (prepared_decode.py:6-94, paged_decode.py:10-112). */
 int moba_hip_decode_fused(const void* q, const void* k, const void* v, int dtype, int Nq, int Hq,
                           int Hkv, int D, void* k_cache, void* v_cache, int page_size, int* table,
                           int table_width, int* lengths, const int* ids, int* positions,
                           const int* delta, void* means, int max_chunks, int chunk, int width,
-                          int R, int dense, int pos_mode, int splits, int* selected,
-                          float* part_o, float* part_ml, void* out, float* lse, void* stream);
+                          int R, int dense, int pos_mode, int splits, const int* sched,
+                          int n_sched, int* selected, float* part_o, float* part_ml, void* out,
+                          float* lse, void* stream);
 
 #ifdef __cplusplus
 }

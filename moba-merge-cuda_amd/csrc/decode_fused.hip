@@ -52,8 +52,11 @@ struct FusedArgs {
   const int* delta;    // [2, Nq] (logical slot, physical page) or null
   uint16_t* means;     // [B, max_chunks, Hkv, D]
   int* selected;       // [Nq, Hq, R + 1] or null
-  float* part_o;       // [Nq, Hq, S, D]
-  float* part_ml;      // [Nq, Hq, S, 2]
+  float* part_o;       // [Nq, Hq, smax, D]
+  float* part_ml;      // [Nq, Hq, smax, 2]
+  const int* sched;    // null: uniform splits; else per workgroup (row x kv head, split,
+                       // splits of that row), then splits per (row x kv head)
+  int n_sched, smax;
   uint16_t* out;       // [Nq, Hq, D]
   float* lse;          // [Nq, Hq]
 };
@@ -82,8 +85,14 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
   __shared__ int s_info[8];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g4 = lane >> 4, c16 = lane & 15;
-  const int split = blockIdx.x, S = gridDim.x;
-  const int rowk = blockIdx.y, qrow = rowk / a.Hkv, kh = rowk % a.Hkv;
+  int split, S, rowk;
+  if (a.sched != nullptr) {
+    const int* e = a.sched + 3 * blockIdx.x;
+    rowk = e[0]; split = e[1]; S = e[2];
+  } else {
+    split = blockIdx.x; S = gridDim.x; rowk = blockIdx.y;
+  }
+  const int qrow = rowk / a.Hkv, kh = rowk % a.Hkv;
   const int G = a.G, D = a.D, C = a.C, width = a.width;
 
   if (tid == 0) {
@@ -243,13 +252,23 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
       for (int x = tid; x < G * nc; x += 64 * kFW) {
         const int g = x / nc, cl = x % nc;
         float acc = 0.0f;
+        // Operands of 8 pieces (64 d) are read in one batch, then the fma
+        // chain runs on registers.  Pieces past D are zero in both staged
+        // rows, and fma(0, 0, acc) == acc, so the chain runs over all DP
+        // without a branch per piece.
+        constexpr int JB = RC < 8 ? RC : 8;
 #pragma unroll
-        for (int j = 0; j < RC; ++j) {
-          if (j * 8 < D) {
-            const u16x8_t mv = ld8(ms + cl * MS + j * 8), qv = ld8(qs + g * DP + j * 8);
+        for (int j0 = 0; j0 < RC; j0 += JB) {
+          u16x8_t mv[JB], qv[JB];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc = fmaf(to_f32<DT>(mv[e]), to_f32<DT>(qv[e]), acc);
+          for (int j = 0; j < JB; ++j) {
+            mv[j] = ld8(ms + cl * MS + (j0 + j) * 8);
+            qv[j] = ld8(qs + g * DP + (j0 + j) * 8);
           }
+#pragma unroll
+          for (int j = 0; j < JB; ++j)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc = fmaf(to_f32<DT>(mv[j][e]), to_f32<DT>(qv[j][e]), acc);
         }
         sc[g * width + c0 + cl] = acc;
       }
@@ -265,12 +284,17 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
       const float v = sg[c];
       if (!(v > -INFINITY)) continue;
       int rank = 0;
-      for (int c0 = 0; c0 < legal && rank < a.R; c0 += 4) {
-        float u[4];
+      // 32 scores per batch, all read before the comparisons; no branches
+      // (reads past `legal` stay inside the route scratch and are masked)
+      for (int c0 = 0; c0 < legal; c0 += 32) {
+        float u[32];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) u[i] = c0 + i < legal ? sg[c0 + i] : -INFINITY;
+        for (int i = 0; i < 32; ++i) u[i] = sg[c0 + i];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) rank += (u[i] > v || (u[i] == v && c0 + i < c)) ? 1 : 0;
+        for (int i = 0; i < 32; ++i) {
+          const int ci = c0 + i;
+          rank += (int)((ci < legal) & ((u[i] > v) | ((u[i] == v) & (ci < c))));
+        }
       }
       if (rank < a.R) {
         sel_s[g * S1 + 1 + rank] = c;
@@ -513,7 +537,7 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
         acc += o[g * DP + d] * f;
       }
     }
-    const int64_t entry = ((int64_t)qrow * a.Hq + kh * G + g) * S + split;
+    const int64_t entry = ((int64_t)qrow * a.Hq + kh * G + g) * a.smax + split;
     a.part_o[entry * D + d] = z > 0.0f ? acc / z : 0.0f;
     if (d == 0) { a.part_ml[2 * entry] = M; a.part_ml[2 * entry + 1] = z; }
   }
@@ -525,9 +549,10 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
 // wave of head 0 also publishes the row's position (and, in step mode,
 // advances its length): every attention workgroup has read it by now.
 template <int DT>
-__global__ __launch_bounds__(64) void merge_kernel(FusedArgs a, int S) {
+__global__ __launch_bounds__(64) void merge_kernel(FusedArgs a) {
   const int lane = threadIdx.x;
   const int rh = blockIdx.x, qrow = rh / a.Hq, h = rh % a.Hq;
+  const int S = a.sched != nullptr ? a.sched[3 * a.n_sched + qrow * a.Hkv + h / a.G] : a.smax;
   const int sid = a.ids[qrow];
   int p;
   if (a.pos_mode == 0) {
@@ -537,7 +562,7 @@ __global__ __launch_bounds__(64) void merge_kernel(FusedArgs a, int S) {
     p = a.pos_mode == 2 ? len : len - 1;
   }
   if (p < 0 || p / a.C > a.width) return;  // the attention launch skipped this row
-  const int64_t e0 = (int64_t)rh * S;
+  const int64_t e0 = (int64_t)rh * a.smax;
   const float m = lane < S ? a.part_ml[2 * (e0 + lane)] : -INFINITY;
   const float z = lane < S ? a.part_ml[2 * (e0 + lane) + 1] : 0.0f;
   const float M = wave_max(z > 0.0f ? m : -INFINITY);
@@ -576,9 +601,10 @@ __global__ __launch_bounds__(64) void merge_kernel(FusedArgs a, int S) {
 
 template <int DT, int DP>
 int launch_fused(const FusedArgs& a, int splits, size_t dyn, hipStream_t st) {
-  dim3 grid((unsigned)splits, (unsigned)(a.Nq * a.Hkv));
+  const dim3 grid = a.sched != nullptr ? dim3((unsigned)a.n_sched)
+                                        : dim3((unsigned)splits, (unsigned)(a.Nq * a.Hkv));
   hipLaunchKernelGGL((fused_kernel<DT, DP>), grid, dim3(64 * kFW), dyn, st, a);
-  hipLaunchKernelGGL((merge_kernel<DT>), dim3((unsigned)(a.Nq * a.Hq)), dim3(64), 0, st, a, splits);
+  hipLaunchKernelGGL((merge_kernel<DT>), dim3((unsigned)(a.Nq * a.Hq)), dim3(64), 0, st, a);
   return moba_launch_status("decode_fused");
 }
 
@@ -603,7 +629,8 @@ extern "C" int moba_hip_decode_fused(const void* q, const void* k, const void* v
                                      int page_size, int* table, int table_width, int* lengths,
                                      const int* ids, int* positions, const int* delta, void* means,
                                      int max_chunks, int chunk, int width, int R, int dense,
-                                     int pos_mode, int splits, int* selected, float* part_o,
+                                     int pos_mode, int splits, const int* sched, int n_sched,
+                                     int* selected, float* part_o,
                                      float* part_ml, void* out, float* lse,
                                      void* stream) {
   if (dtype != 0 && dtype != 1) { moba_set_error("decode_fused: dtype must be 0 (bf16) or 1 (fp16)"); return MOBA_ERR_ARG; }
@@ -614,6 +641,7 @@ extern "C" int moba_hip_decode_fused(const void* q, const void* k, const void* v
   if (R < 0 || R + 1 > kMaxSlots) { moba_set_error("decode_fused: routed chunk count must be in [0,8]"); return MOBA_ERR_ARG; }
   if (pos_mode < 0 || pos_mode > 2) { moba_set_error("decode_fused: pos_mode must be 0 (given), 1 (attend) or 2 (step)"); return MOBA_ERR_ARG; }
   if (splits < 1 || splits > 64) { moba_set_error("decode_fused: splits must be in [1,64]"); return MOBA_ERR_ARG; }
+  if (sched != nullptr && n_sched < Nq * Hkv) { moba_set_error("decode_fused: a schedule needs at least one workgroup per (row, kv head)"); return MOBA_ERR_ARG; }
   if (page_size < 1 || chunk < 1 || width < 0 || Nq < 1) { moba_set_error("decode_fused: bad sizes"); return MOBA_ERR_ARG; }
   if (pos_mode == 2 && (k == nullptr || v == nullptr)) { moba_set_error("decode_fused: step mode needs the new K/V rows"); return MOBA_ERR_ARG; }
   FusedArgs a;
@@ -626,6 +654,7 @@ extern "C" int moba_hip_decode_fused(const void* q, const void* k, const void* v
   a.table = table; a.lengths = lengths; a.ids = ids; a.positions = positions; a.delta = delta;
   a.means = (uint16_t*)means; a.selected = selected; a.part_o = part_o; a.part_ml = part_ml;
   a.out = (uint16_t*)out; a.lse = lse;
+  a.sched = sched; a.n_sched = n_sched; a.smax = splits;
   const size_t dyn = fused_route_lds(a.G, width);
   hipStream_t st = (hipStream_t)stream;
   return dtype == 0 ? dispatch_fused<0>(a, splits, dyn, st) : dispatch_fused<1>(a, splits, dyn, st);

@@ -40,7 +40,7 @@ SIGNATURES = {
                              _I, _P],
     "moba_hip_decode_fused_supported": [_I, _I, _I, _I, _I],
     "moba_hip_decode_fused": [_P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _I, _P, _P, _P, _P,
-                              _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P],
+                              _P, _I, _I, _I, _I, _I, _I, _I, _P, _I, _P, _P, _P, _P, _P, _P],
 }
 _RESTYPES = {"moba_hip_last_error": ctypes.c_char_p}
 

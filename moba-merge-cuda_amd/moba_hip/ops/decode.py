@@ -92,15 +92,98 @@ def fused_splits(nq, hkv) -> int:
     return max(1, min(64, -(-512 // (nq * hkv))))
 
 
-class FusedWork:
-    """Persistent workspaces of ``fused``: the split partials."""
-    __slots__ = ("splits", "part_o", "part_ml")
+# Workgroups of a scheduled decode launch (two per CU) and the split cap.
+SCHED_WORKGROUPS = 512
+SCHED_MAX_SPLITS = 64
 
-    def __init__(self, nq, hq, hkv, d, device, splits=None):
-        self.splits = splits or fused_splits(nq, hkv)
+
+def expected_union_tokens(pos, group, remote, chunk, dense=False) -> float:
+    """Expected tokens a (row, kv head) attends at position ``pos``: the
+    current chunk up to pos, plus the closed chunks that at least one of the
+    ``group`` q heads selects when each picks ``remote`` of the closed chunks
+    (the expected coverage of independent uniform picks)."""
+    if dense:
+        return float(pos + 1)
+    cur = pos // chunk
+    own = pos - cur * chunk + 1
+    if cur == 0 or remote == 0:
+        return float(own)
+    picks = min(remote, cur)
+    covered = cur * (1.0 - (1.0 - picks / cur) ** group)
+    return own + chunk * covered
+
+
+def sched_workgroups(nq, hkv, workgroups=SCHED_WORKGROUPS, max_splits=SCHED_MAX_SPLITS) -> int:
+    """Grid size of a scheduled launch: fixed for a given batch shape."""
+    rows = nq * hkv
+    return max(rows, min(workgroups, rows * max_splits))
+
+
+def fused_schedule(positions, hkv, group, remote, chunk, dense=False,
+                   workgroups=SCHED_WORKGROUPS, max_splits=SCHED_MAX_SPLITS):
+    """Split counts per (row, kv head) proportional to the expected attended
+    tokens (largest remainders, each in [1, max_splits]) over exactly
+    ``sched_workgroups`` workgroups.  Returns (schedule int32 list for
+    moba_hip_decode_fused: the workgroup entries (row * hkv + kv head, split,
+    splits of that row), interleaved across rows, then the split counts;
+    the split counts; the number of workgroups)."""
+    rows = len(positions) * hkv
+    total = sched_workgroups(len(positions), hkv, workgroups, max_splits)
+    weights = []
+    for p in positions:
+        w = expected_union_tokens(max(0, int(p)), group, remote, chunk, dense)
+        weights += [max(w, 1.0)] * hkv
+    splits = [1] * rows
+    free = total - rows
+    active = list(range(rows))
+    while free > 0 and active:
+        wsum = sum(weights[i] for i in active)
+        share = {i: free * weights[i] / wsum for i in active}
+        grant = {i: min(int(share[i]), max_splits - splits[i]) for i in active}
+        given = sum(grant.values())
+        for i in sorted(active, key=lambda i: share[i] - int(share[i]), reverse=True):
+            if given >= free:
+                break
+            if splits[i] + grant[i] < max_splits:
+                grant[i] += 1
+                given += 1
+        for i in active:
+            splits[i] += grant[i]
+        free -= given
+        active = [i for i in active if splits[i] < max_splits]
+    entries = []
+    for sidx in range(max(splits)):  # interleave rows across the launch
+        for r in range(rows):
+            if sidx < splits[r]:
+                entries += [r, sidx, splits[r]]
+    return entries + splits, splits, total
+
+
+class FusedWork:
+    """Persistent workspaces of ``fused``: the split partials, and with
+    ``scheduled`` a device schedule of ``sched_workgroups`` workgroups (see
+    ``fused_schedule``) that the owner refreshes between launches."""
+    __slots__ = ("splits", "part_o", "part_ml", "sched", "sched_host", "n_sched", "sched_splits")
+
+    def __init__(self, nq, hq, hkv, d, device, splits=None, scheduled=False):
+        self.splits = splits or (SCHED_MAX_SPLITS if scheduled else fused_splits(nq, hkv))
         n = nq * hq * self.splits
         self.part_o = torch.empty((n, d), dtype=torch.float32, device=device)
         self.part_ml = torch.empty((n, 2), dtype=torch.float32, device=device)
+        self.sched = self.sched_host = self.sched_splits = None
+        self.n_sched = 0
+        if scheduled:
+            self.n_sched = sched_workgroups(nq, hkv, max_splits=self.splits)
+            size = 3 * self.n_sched + nq * hkv
+            self.sched = torch.zeros(size, dtype=torch.int32, device=device)
+            self.sched_host = torch.zeros(size, dtype=torch.int32, pin_memory=True)
+
+    def set_schedule(self, entries, splits):
+        """Uploads a schedule of n_sched workgroups (synchronous tiny copy)."""
+        assert len(entries) == len(self.sched_host)
+        self.sched_host.copy_(torch.tensor(entries, dtype=torch.int32))
+        self.sched.copy_(self.sched_host, non_blocking=False)
+        self.sched_splits = list(splits)
 
 
 def fused_args(q, k, v, kc, vc, table, lengths, ids, positions, delta, means, chunk, width,
@@ -112,8 +195,8 @@ def fused_args(q, k, v, kc, vc, table, lengths, ids, positions, delta, means, ch
             kc.data_ptr(), vc.data_ptr(), kc.shape[1], table.data_ptr(), table.shape[1],
             lengths.data_ptr(), ids.data_ptr(), positions.data_ptr(), _lib.ptr(delta),
             means.data_ptr(), means.shape[1], chunk, width, remote, 1 if dense else 0, pos_mode,
-            work.splits, _lib.ptr(selected), work.part_o.data_ptr(), work.part_ml.data_ptr(),
-            out.data_ptr(), lse.data_ptr())
+            work.splits, _lib.ptr(work.sched), work.n_sched, _lib.ptr(selected),
+            work.part_o.data_ptr(), work.part_ml.data_ptr(), out.data_ptr(), lse.data_ptr())
 
 
 def launch_fused(args, stream):

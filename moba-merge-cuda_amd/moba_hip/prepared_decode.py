@@ -74,13 +74,17 @@ class PreparedDecode:
             self._part_o = torch.empty((n, d), device=dev, dtype=torch.float32)
             self._part_ml = torch.empty((n, 2), device=dev, dtype=torch.float32)
             # one-launch step (route + attention + append) when the shape allows
-            self._fused = (kernels.FusedWork(b, h, cache.num_kv_heads, d, dev)
+            # split counts per row follow each row's expected attended tokens
+            self._fused = (kernels.FusedWork(b, h, cache.num_kv_heads, d, dev, scheduled=True)
                            if kernels.fused_supported(h, cache.num_kv_heads, d, width, cache._table.shape[1]) else None)
+            self._sched_pos = None
             self._fused_args = None
             self.gpu_ids = torch.tensor(self.ids, device=dev, dtype=torch.int32)
             self.positions = torch.empty(b, device=dev, dtype=torch.int32)
             self.delta = torch.full((2, b), -1, device=dev, dtype=torch.int32)
             self.delta_host = torch.empty((2, b), dtype=torch.int32, pin_memory=True)
+            if self._fused is not None:  # every launch reads a valid schedule
+                self._schedule([self._state.lengths[s] for s in self.ids])
             table, lengths = cache._table.clone(), cache._lengths.clone()
             # publish the exclusive lease only after every allocation succeeded
             cache._table, cache._lengths = table, lengths
@@ -138,6 +142,22 @@ class PreparedDecode:
         self.delta.copy_(self.delta_host, non_blocking=False)
         self.delta_uploads += 1
 
+    def _schedule(self, positions):
+        """Refreshes the fused launch's split schedule when some row's
+        position moved by more than 1/8 since the last upload."""
+        if self._fused is None:
+            return
+        old = self._sched_pos
+        if old is not None and all(abs(p - o) * 8 <= max(o, 1) for p, o in zip(positions, old)):
+            return
+        c = self.cache
+        entries, splits, _ = kernels.fused_schedule(
+            positions, c.num_kv_heads, self.num_q_heads // c.num_kv_heads, self.remote,
+            c.chunk_size, self.dense, max_splits=self._fused.splits)
+        if splits != self._fused.sched_splits:
+            self._fused.set_schedule(entries, splits)
+        self._sched_pos = list(positions)
+
     def _compute(self, append):
         c = self.cache
         if self._fused is not None:
@@ -193,6 +213,7 @@ class PreparedDecode:
                 raise ValueError("capture('attend') first")
             if q is not self.q:
                 self.q.copy_(q)
+            self._schedule(pos)
             self._run("attend", use_graph)
             return self._result(pos)
 
@@ -210,6 +231,7 @@ class PreparedDecode:
                 if tensor is not target:
                     target.copy_(tensor)
             self._upload(plan)
+            self._schedule(plan.positions)
             self._run("step", use_graph)
             self._state.commit(plan)
             return self._result(plan.positions)
@@ -235,6 +257,8 @@ class PreparedDecode:
             try:
                 if plan is not None:
                     self._upload(plan)
+                self._schedule(plan.positions if plan is not None
+                               else [self._state.lengths[s] - 1 for s in self.ids])
                 side.wait_stream(main)
                 with torch.cuda.stream(side):
                     for _ in range(2):  # warm-up outside the graph

@@ -105,3 +105,29 @@ def test_incremental_failures_do_not_mutate():
     old.commit(old.plan_append([0], [1]))
     with pytest.raises(ValueError, match="max_seq_len"):
         IncrementalLayout(old, [0]).plan()
+
+
+def test_fused_schedule_covers_every_split_once():
+    """Decode split schedule: every (row, kv head) gets 1..max splits, each
+    split exactly once, over a fixed grid; longer rows get more splits."""
+    from moba_hip.ops.decode import fused_schedule, sched_workgroups, expected_union_tokens
+    for positions, hkv, group, remote, chunk in (
+            ([15883, 8359, 14466, 8938, 2711, 6290, 10424, 10009], 2, 6, 3, 512),
+            ([0, 5, 31000, 2000] * 8, 1, 16, 7, 1024),
+            ([3, 4], 2, 4, 2, 4)):
+        entries, splits, n = fused_schedule(positions, hkv, group, remote, chunk)
+        rows = len(positions) * hkv
+        assert n == sched_workgroups(len(positions), hkv)
+        assert len(entries) == 3 * n + rows and entries[3 * n:] == splits
+        assert sum(splits) == n and all(1 <= s <= 64 for s in splits)
+        seen = set()
+        for w in range(n):
+            r, s, c = entries[3 * w: 3 * w + 3]
+            assert c == splits[r] and 0 <= s < c and (r, s) not in seen
+            seen.add((r, s))
+        assert len(seen) == n
+        w = [expected_union_tokens(positions[r // hkv], group, remote, chunk) for r in range(rows)]
+        for a in range(rows):
+            for b in range(rows):
+                if w[a] > 1.5 * w[b] and splits[b] < 64:
+                    assert splits[a] >= splits[b]
