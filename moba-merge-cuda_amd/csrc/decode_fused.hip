@@ -17,8 +17,8 @@
 // from the page pool, heads that did not select the block's chunk masked),
 // O^T += V^T P^T with V^T from a wave-private LDS tile by the transposed read.
 // The waves merge in LDS into one (o, max, sum) partial per (head, split).
-// merge_kernel, one wave per (query, q head), then combines the S partials in
-// split order (deterministic for a fixed S).  The launch boundary orders the
+// merge_kernel, one workgroup per (query, q head), then combines the S
+// partials in a fixed order (deterministic for a fixed S).  The launch boundary orders the
 // partial stores before the merge reads, with no device-scope fences or
 // arrival counters inside either kernel.
 //
@@ -545,12 +545,18 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
 
 // Combines the S split partials of one (query, q head): weights
 // w_s = z_s 2^(m_s - M), O = sum w_s o_s / sum w_s, LSE = M + log2(sum w_s)
-// (natural log on output), summed in split order.  In prepared modes the
-// wave of head 0 also publishes the row's position (and, in step mode,
-// advances its length): every attention workgroup has read it by now.
+// (natural log on output).  Wave w takes splits w, w + 4, ...: every partial
+// load is issued before any arithmetic.
+// Each wave sums its splits in order, then the 4 wave sums are added in wave
+// order (deterministic for a fixed S).  In prepared modes head 0 also
+// publishes the row's position (and, in step mode, advances its length):
+// every attention workgroup has read it by now.
+constexpr int kMergeWaves = 4;
+constexpr int kMergePer = 64 / kMergeWaves;  // splits per wave (S <= 64)
+
 template <int DT>
-__global__ __launch_bounds__(64) void merge_kernel(FusedArgs a) {
-  const int lane = threadIdx.x;
+__global__ __launch_bounds__(64 * kMergeWaves) void merge_kernel(FusedArgs a) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int rh = blockIdx.x, qrow = rh / a.Hq, h = rh % a.Hq;
   const int S = a.sched != nullptr ? a.sched[3 * a.n_sched + qrow * a.Hkv + h / a.G] : a.smax;
   const int sid = a.ids[qrow];
@@ -563,31 +569,55 @@ __global__ __launch_bounds__(64) void merge_kernel(FusedArgs a) {
   }
   if (p < 0 || p / a.C > a.width) return;  // the attention launch skipped this row
   const int64_t e0 = (int64_t)rh * a.smax;
-  const float m = lane < S ? a.part_ml[2 * (e0 + lane)] : -INFINITY;
-  const float z = lane < S ? a.part_ml[2 * (e0 + lane) + 1] : 0.0f;
-  const float M = wave_max(z > 0.0f ? m : -INFINITY);
-  const float wgt = z > 0.0f ? z * fast_exp2(m - M) : 0.0f;
-  __shared__ float ws[64];
-  ws[lane] = wgt;
-  __builtin_amdgcn_wave_barrier();
-  // Z in split order (a fixed-order sum, not a tree)
-  float Z = 0.0f;
-  for (int s = 0; s < S; ++s) Z += ws[s];
   const int d = lane * 4;
-  if (d < a.D) {
-    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-    const f32x4_t* po = reinterpret_cast<const f32x4_t*>(a.part_o + e0 * a.D + d);
-#pragma unroll 16
-    for (int s = 0; s < S; ++s) {
-      const f32x4_t o = po[(int64_t)s * (a.D / 4)];
-      const float wv = ws[s];
+  const bool dok = d < a.D;
+  float m[kMergePer], z[kMergePer];
+  f32x4_t o[kMergePer];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] += wv * o[i];
-    }
+  for (int i = 0; i < kMergePer; ++i) {
+    const int s = w + kMergeWaves * i;
+    const bool ok = s < S;
+    m[i] = ok ? a.part_ml[2 * (e0 + s)] : -INFINITY;
+    z[i] = ok ? a.part_ml[2 * (e0 + s) + 1] : 0.0f;
+    o[i] = (ok && dok) ? *reinterpret_cast<const f32x4_t*>(a.part_o + (e0 + s) * a.D + d)
+                       : (f32x4_t){0.f, 0.f, 0.f, 0.f};
+  }
+  __shared__ float wm[kMergeWaves], wz[kMergeWaves];
+  __shared__ f32x4_t wo[kMergeWaves][64];
+  float mw = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < kMergePer; ++i) mw = fmaxf(mw, z[i] > 0.0f ? m[i] : -INFINITY);
+  if (lane == 0) wm[w] = mw;
+  __syncthreads();
+  float M = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < kMergeWaves; ++i) M = fmaxf(M, wm[i]);
+  float Zw = 0.0f;
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < kMergePer; ++i) {
+    const float wt = z[i] > 0.0f ? z[i] * fast_exp2(m[i] - M) : 0.0f;
+    Zw += wt;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] += wt * o[i][e];
+  }
+  wo[w][lane] = acc;
+  if (lane == 0) wz[w] = Zw;
+  __syncthreads();
+  if (w != 0) return;
+  float Z = 0.0f;
+  f32x4_t tot = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < kMergeWaves; ++i) {
+    Z += wz[i];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tot[e] += wo[i][lane][e];
+  }
+  if (dok) {
     const float iz = Z > 0.0f ? 1.0f / Z : 0.0f;
     u16x4_t r;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = from_f32<DT>(acc[i] * iz);
+    for (int e = 0; e < 4; ++e) r[e] = from_f32<DT>(tot[e] * iz);
     *reinterpret_cast<u16x4_t*>(a.out + (int64_t)rh * a.D + d) = r;
   }
   if (lane == 0) {
@@ -604,7 +634,7 @@ int launch_fused(const FusedArgs& a, int splits, size_t dyn, hipStream_t st) {
   const dim3 grid = a.sched != nullptr ? dim3((unsigned)a.n_sched)
                                         : dim3((unsigned)splits, (unsigned)(a.Nq * a.Hkv));
   hipLaunchKernelGGL((fused_kernel<DT, DP>), grid, dim3(64 * kFW), dyn, st, a);
-  hipLaunchKernelGGL((merge_kernel<DT>), dim3((unsigned)(a.Nq * a.Hq)), dim3(64), 0, st, a);
+  hipLaunchKernelGGL((merge_kernel<DT>), dim3((unsigned)(a.Nq * a.Hq)), dim3(64 * kMergeWaves), 0, st, a);
   return moba_launch_status("decode_fused");
 }
 
