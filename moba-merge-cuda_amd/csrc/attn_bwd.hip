@@ -375,7 +375,9 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t G1[BQ * DP];
   __shared__ __attribute__((aligned(16))) float lse2s[2][BQ];
   __shared__ __attribute__((aligned(16))) float dels[2][BQ];
-  __shared__ float Ps[4][QB][16][64];         // P handed from role P to role D
+  // P (input dtype, the same rounding dV uses) handed from role P to role D:
+  // [pair][qb][half][lane], 8 values per lane
+  __shared__ __attribute__((aligned(16))) u16x8_t Px[4][QB][2][64];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int qi = lane & 31, hh = lane >> 5;
@@ -490,14 +492,28 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
       // ---- first half: S -> P (role P) or dP (role D)
       const uint16_t* A1 = ROLE_P ? Qb : Gb;
       f32x16_t sp[QB];
+      u16x8_t pk[QB][2];  // role P: P as the A operand of dV += P^T dO
       if (!skip) {
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) sp[qb] = zero16();
+        // operand reads run PF steps ahead of the MFMAs, in this order (the
+        // scheduling fences keep the compiler from sinking them)
+        {
+          constexpr int N1 = NKS * QB, PF = 6;
+          u16x8_t ring[PF];
+          auto rd = [&](int i) __attribute__((always_inline)) {
+            return lds8(A1, (i % QB) * 32 * DP * 2 + swz_b128<DP>(kq, i / QB));
+          };
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks)
+          for (int i = 0; i < PF && i < N1; ++i) ring[i] = rd(i);
 #pragma unroll
-          for (int qb = 0; qb < QB; ++qb)
-            sp[qb] = mfma32<DT>(lds8(A1, qb * 32 * DP * 2 + swz_b128<DP>(kq, ks)), kv[ks], sp[qb]);
+          for (int i = 0; i < N1; ++i) {
+            const u16x8_t x = ring[i % PF];
+            if (i + PF < N1) ring[i % PF] = rd(i + PF);
+            sp[i % QB] = mfma32<DT>(x, kv[i / QB], sp[i % QB]);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
         if constexpr (ROLE_P) {
           auto to_p = [&](auto mask_tag) {
             constexpr bool MASK = decltype(mask_tag)::value;
@@ -512,12 +528,16 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
                   float p = fast_exp2(fmaf(sp[qb][4 * j + i], c2, -l4[i]));
                   if constexpr (MASK)
                     p = (mykey < c_hi && (!is_self || mykey <= sq0 + r0 + i)) ? p : 0.0f;
-                  sp[qb][4 * j + i] = p;
-                  Ps[pair][qb][4 * j + i][lane] = p;
+                  pk[qb][j >> 1][(j & 1) * 4 + i] = from_f32<DT>(p);
                 }
               }
           };
           if (need_mask) to_p(std::true_type{}); else to_p(std::false_type{});
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) {
+            Px[pair][qb][0][lane] = pk[qb][0];
+            Px[pair][qb][1][lane] = pk[qb][1];
+          }
         }
       }
       lds_barrier();
@@ -526,35 +546,43 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
         u16x8_t op[QB][2];
         if constexpr (ROLE_P) {
 #pragma unroll
-          for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) op[qb][r >> 3][r & 7] = from_f32<DT>(sp[qb][r]);
+          for (int qb = 0; qb < QB; ++qb) { op[qb][0] = pk[qb][0]; op[qb][1] = pk[qb][1]; }
         } else {
 #pragma unroll
-          for (int qb = 0; qb < QB; ++qb)
+          for (int qb = 0; qb < QB; ++qb) {
+            const u16x8_t px[2] = {Px[pair][qb][0][lane], Px[pair][qb][1][lane]};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
               const f32x4_t d4 =
                   *reinterpret_cast<const f32x4_t*>(&dels[buf][qb * 32 + 8 * j + 4 * hh]);
 #pragma unroll
               for (int i = 0; i < 4; ++i) {
-                const int r = 4 * j + i;
-                const float p = Ps[pair][qb][r][lane];
-                op[qb][j >> 1][(j & 1) * 4 + i] = from_f32<DT>(p * (sp[qb][r] - d4[i]));
+                const int r = 4 * j + i, h2 = j >> 1, x = (j & 1) * 4 + i;
+                op[qb][h2][x] = from_f32<DT>(to_f32<DT>(px[h2][x]) * (sp[qb][r] - d4[i]));
               }
             }
+          }
         }
         const uint16_t* B2 = ROLE_P ? Gb : Qb;
+        {
+          constexpr int N2 = NDB * QB * 2, PF = 6;
+          u16x8_t ring[PF];
+          // step i: d block i / (2 QB), row block (i / 2) % QB, half i % 2
+          auto rd = [&](int i) __attribute__((always_inline)) {
+            const uint32_t ro = (((i / 2) % QB) * 32 + (i % 2) * 16) * DP * 2;
+            const int db = i / (2 * QB);
+            return lds_tr8(B2, ro + swz_tr<DP>(t0, db), ro + swz_tr<DP>(t1, db));
+          };
 #pragma unroll
-        for (int i = 0; i < NDB; ++i)
+          for (int i = 0; i < PF && i < N2; ++i) ring[i] = rd(i);
 #pragma unroll
-          for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-              const uint32_t ro = (qb * 32 + t * 16) * DP * 2;
-              acc[i] = mfma32<DT>(op[qb][t],
-                                  lds_tr8(B2, ro + swz_tr<DP>(t0, i), ro + swz_tr<DP>(t1, i)), acc[i]);
-            }
+          for (int i = 0; i < N2; ++i) {
+            const u16x8_t b = ring[i % PF];
+            if (i + PF < N2) ring[i % PF] = rd(i + PF);
+            acc[i / (2 * QB)] = mfma32<DT>(op[(i / 2) % QB][i % 2], b, acc[i / (2 * QB)]);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
       }
     };
 
