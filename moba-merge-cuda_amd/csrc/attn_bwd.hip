@@ -206,14 +206,43 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a
       f32x16_t sa[QB], pa[QB];
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) { sa[qb] = zero16(); pa[qb] = zero16(); }
+      if constexpr (REMOTE) {
+        // the expert variant holds more per-row state: no room for a ring
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) {
-        const uint32_t o = kb * 32 * DP * 2 + swz_b128<DP>(kq, ks);
-        const u16x8_t ka = lds8(Kb, o), va = lds8(Vb, o);
+        for (int ks = 0; ks < NKS; ++ks) {
+          const uint32_t o = kb * 32 * DP * 2 + swz_b128<DP>(kq, ks);
+          const u16x8_t ka = lds8(Kb, o), va = lds8(Vb, o);
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-          sa[qb] = mfma32<DT>(ka, qf[qb][ks], sa[qb]);
-          pa[qb] = mfma32<DT>(va, gf[qb][ks], pa[qb]);
+          for (int qb = 0; qb < QB; ++qb) {
+            sa[qb] = mfma32<DT>(ka, qf[qb][ks], sa[qb]);
+            pa[qb] = mfma32<DT>(va, gf[qb][ks], pa[qb]);
+          }
+        }
+      } else {
+        // K / V operand reads run PF k-steps ahead of the MFMAs, in this
+        // order (the scheduling fences keep the compiler from sinking them)
+        constexpr int PF = 3;
+        u16x8_t rk[PF], rv[PF];
+#pragma unroll
+        for (int i = 0; i < PF && i < NKS; ++i) {
+          const uint32_t o = kb * 32 * DP * 2 + swz_b128<DP>(kq, i);
+          rk[i] = lds8(Kb, o);
+          rv[i] = lds8(Vb, o);
+        }
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+          const u16x8_t ka = rk[ks % PF], va = rv[ks % PF];
+          if (ks + PF < NKS) {
+            const uint32_t o = kb * 32 * DP * 2 + swz_b128<DP>(kq, ks + PF);
+            rk[ks % PF] = lds8(Kb, o);
+            rv[ks % PF] = lds8(Vb, o);
+          }
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) {
+            sa[qb] = mfma32<DT>(ka, qf[qb][ks], sa[qb]);
+            pa[qb] = mfma32<DT>(va, gf[qb][ks], pa[qb]);
+          }
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
       u16x8_t dsv[QB][2];
@@ -233,33 +262,54 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a
         dsv[qb][0] = pack8<DT>(tmp);
         dsv[qb][1] = pack8<DT>(tmp + 8);
       }
+      if constexpr (REMOTE) {
 #pragma unroll
-      for (int db = 0; db < NDB; ++db)
+        for (int db = 0; db < NDB; ++db)
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const uint32_t ro = (kb * 32 + t * 16) * DP * 2;
-          const u16x8_t kt = lds_tr8(Kb, ro + swz_tr<DP>(t0, db), ro + swz_tr<DP>(t1, db));
+          for (int t = 0; t < 2; ++t) {
+            const uint32_t ro = (kb * 32 + t * 16) * DP * 2;
+            const u16x8_t kt = lds_tr8(Kb, ro + swz_tr<DP>(t0, db), ro + swz_tr<DP>(t1, db));
 #pragma unroll
-          for (int qb = 0; qb < QB; ++qb) acc[qb][db] = mfma32<DT>(kt, dsv[qb][t], acc[qb][db]);
-        }
-      // Issue order for this 32-key block: LDS operand reads run at most two
-      // MFMAs ahead, which bounds the registers they hold.
-      if constexpr (QB == 1) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+            for (int qb = 0; qb < QB; ++qb) acc[qb][db] = mfma32<DT>(kt, dsv[qb][t], acc[qb][db]);
+          }
+        // issue order for this 32-key block: LDS operand reads run at most
+        // two MFMAs ahead, which bounds the registers they hold
+        if constexpr (QB == 1) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-        for (int i = 0; i < NKS - 2; ++i) {
+          for (int i = 0; i < NKS - 2; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+          }
+          __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 200, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+          for (int i = 0; i < 2 * NDB - 2; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+          }
           __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-          __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 200, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+      } else {
+        // K^T operand reads pipelined the same way; step i is d block i / 2
+        // of 16-key half i % 2
+        constexpr int N2 = 2 * NDB, PF = 4;
+        u16x8_t ring[PF];
+        auto rd = [&](int i) __attribute__((always_inline)) {
+          const uint32_t ro = (kb * 32 + (i % 2) * 16) * DP * 2;
+          return lds_tr8(Kb, ro + swz_tr<DP>(t0, i / 2), ro + swz_tr<DP>(t1, i / 2));
+        };
 #pragma unroll
-        for (int i = 0; i < 2 * NDB - 2; ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        for (int i = 0; i < PF && i < N2; ++i) ring[i] = rd(i);
+#pragma unroll
+        for (int i = 0; i < N2; ++i) {
+          const u16x8_t kt = ring[i % PF];
+          if (i + PF < N2) ring[i % PF] = rd(i + PF);
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) acc[qb][i / 2] = mfma32<DT>(kt, dsv[qb][i % 2], acc[qb][i / 2]);
+          __builtin_amdgcn_sched_barrier(0);
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
