@@ -96,7 +96,7 @@ int moba_hip_prefill_fwd(const void* q, const void* k, const void* v, int dtype,
  * filtered index or -1, kv head): one workgroup per entry, tiles of 128
  * keys; chunk -1 marks an empty entry.  delta [2*T*Hq] and
  * part_dq [T*Hq*R, D] fp32 are workspaces.  pack is a workspace of
- * T*Hq*R*(4*D + 8) bytes for parts & 2 when R > 0 and D <= 64 (the expert
+ * T*Hq*R*(4*D + 8) bytes for parts & 2 when R > 0 and D <= 128 (the expert
  * rows of q, dO, lse and delta copied contiguously), else may be NULL.  dq [T,Hq,D], dk/dv [T,Hkv,D]
  * (dtype) are fully written (every key belongs to exactly one kv tile).
  * parts selects the launches: 1 = Delta and dq (query-major kernels), 2 = dk/dv

@@ -734,12 +734,13 @@ int launch_bwd(const BwdArgs& a, int n_self, int n_kv, int max_remote, int parts
   }
   if ((parts & 2) && n_kv > 0) {
     // 128 keys per workgroup in both kernels; the host's key tiles match
-    if constexpr (DP <= 64) {
+    if constexpr (DP <= 128) {
       if (a.pack_rows > 0) {
         const int64_t pieces = a.pack_rows * (a.D / 8);
         hipLaunchKernelGGL(pack_rows_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, st, a);
       }
-      launch_dkdv1<DT, DP>(a, n_kv, st);
+      if constexpr (DP <= 64) launch_dkdv1<DT, DP>(a, n_kv, st);
+      else launch_dkdv2<DT, DP>(a, n_kv, st);
     } else {
       hipLaunchKernelGGL((dkdv_kernel<DT, DP>), dim3(n_kv, a.kv_splits), dim3(512), 0, st, a);
     }
@@ -790,12 +791,12 @@ extern "C" int moba_hip_prefill_bwd(const void* q, const void* k, const void* v,
   a.delta = delta; a.part_dq = part_dq; a.part_dkv = part_dkv; a.kv_splits = kv_splits;
   a.dq = (uint16_t*)dq; a.dk = (uint16_t*)dk; a.dv = (uint16_t*)dv;
   a.lse2 = delta + (int64_t)T * Hq;
-  a.pack_rows = (R > 0 && D <= 64) ? (int64_t)T * Hq * R : 0;
+  a.pack_rows = (R > 0 && D <= 128) ? (int64_t)T * Hq * R : 0;
   a.pack_q = (uint16_t*)pack;
   a.pack_g = a.pack_q + a.pack_rows * D;
   a.pack_lse2 = (float*)(a.pack_g + a.pack_rows * D);
   a.pack_delta = a.pack_lse2 + a.pack_rows;
-  if (a.pack_rows > 0 && (parts & 2) && pack == nullptr) { moba_set_error("prefill_bwd: the pack workspace is required when R > 0 and head_dim <= 64"); return MOBA_ERR_ARG; }
+  if (a.pack_rows > 0 && (parts & 2) && pack == nullptr) { moba_set_error("prefill_bwd: the pack workspace is required when R > 0 and head_dim <= 128"); return MOBA_ERR_ARG; }
   if (a.pack_rows * D * 2 >= ((int64_t)1 << 32)) { moba_set_error("prefill_bwd: packed expert rows must be smaller than 4 GiB (32-bit buffer offsets)"); return MOBA_ERR_ARG; }
   hipStream_t st = (hipStream_t)stream;
   const int mr = R > 0 ? max_remote_tiles : 0;

@@ -1,0 +1,333 @@
+// Key-major dK / dV of the MoBA prefill backward for head dims 65..128:
+// wave pairs with split roles and a one-tile lag, no barrier inside a tile.
+//
+// Replaces the dk/dv halves of the two flash-attention backwards in
+// OptMixedAttention.backward (src/moba_opt/mixed_attention.py:165-221) and the
+// autograd scatter-add of the packed remote dk/dv into k/v
+// (grouped_attention.py:81-89): every query row that attends a key -- the
+// causal rows of the key's own chunk for all G heads of its KV group, then the
+// expert rows that selected the chunk -- is visited by the one workgroup that
+// owns the key, so dK / dV are summed in registers in a fixed order and
+// written once (no atomics).
+//
+// A workgroup of 8 waves owns 128 keys of one chunk and one KV head as 4 wave
+// pairs of 32 keys; the two waves of a pair share a SIMD.  For 64-row tiles
+// of (Q, dO) rows:
+//   role P (K in registers, dV accumulators), at tile i:
+//       S = Q_i K^T, P = exp2(S*c - lse2) -> LDS (input dtype), dV += P^T dO_i
+//   role D (V in registers, dK accumulators), at tile i:
+//       dS_{i-1} = P_{i-1} (dP_{i-1} - delta), dK += dS^T Q_{i-1}  (P from LDS)
+//       dP_i = dO_i V^T                        (kept in registers for i + 1)
+// Role D runs one tile behind role P on the P it needs, so the only
+// synchronisation is the barrier where the LDS stages rotate: P_{i-1} was
+// written before it.  Three stages hold tiles i - 1 (role D's Q), i and
+// i + 1 (loading).  The expert rows come packed contiguously (pack_rows_kernel),
+// so every tile is affine in the row number and is loaded HBM -> LDS by
+// buffer loads issued from inline assembly (the waits are placed here).
+#include <type_traits>
+
+#include "common.h"
+#include "bwd_args.h"
+
+namespace moba {
+namespace {
+
+constexpr int kPairKeys = 32;   // keys per wave pair
+constexpr int kRows = 64;       // query rows per tile
+
+template <int DT, int DP>
+__global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
+  constexpr int NKS = DP / 16, NDB = DP / 32, QB = kRows / 32;
+  constexpr int NB = DP / 8;                    // 16-byte blocks per row
+  constexpr int NDMA = kRows * NB / 512;        // blocks per thread per operand
+  static_assert(NDMA >= 1 && kRows * NB % 512 == 0, "one block per thread at least");
+  // Q / dO tiles (swz<DP> layout) and their rows' lse2 / delta, three named
+  // stages; P of the last two tiles per pair: [tile & 1][pair][qb][half][lane].
+  __shared__ __attribute__((aligned(16))) uint16_t Q0[kRows * DP];
+  __shared__ __attribute__((aligned(16))) uint16_t G0[kRows * DP];
+  __shared__ __attribute__((aligned(16))) uint16_t Q1[kRows * DP];
+  __shared__ __attribute__((aligned(16))) uint16_t G1[kRows * DP];
+  __shared__ __attribute__((aligned(16))) uint16_t Q2[kRows * DP];
+  __shared__ __attribute__((aligned(16))) uint16_t G2[kRows * DP];
+  __shared__ __attribute__((aligned(16))) float L0[2 * kRows];
+  __shared__ __attribute__((aligned(16))) float L1[2 * kRows];
+  __shared__ __attribute__((aligned(16))) float L2[2 * kRows];
+  __shared__ __attribute__((aligned(16))) u16x8_t Px[2][4][QB][2][64];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int qi = lane & 31, hh = lane >> 5;
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  const int pair = wave & 3;
+  const bool role_p = wave < 4;
+  const int D = a.D, G = a.G;
+  const int* tile = a.kv_tiles + 4 * blockIdx.x;
+  const int c = tile[0], kt0 = tile[1], f = tile[2], kh = tile[3];
+  if (c < 0) return;                          // padding entry of the XCD-ordered list
+  const int c_lo = a.cu_chunk[c], c_hi = a.cu_chunk[c + 1];
+  const int key0 = c_lo + kt0;                // first key of the workgroup
+  const int pkey0 = key0 + pair * kPairKeys;  // first key of this pair
+  const int mykey = pkey0 + qi;               // this lane's key (B operand column)
+
+  // Uninitialised LDS could hold NaN patterns that a zero probability would
+  // not cancel; column blocks past D are never loaded and must read zero.
+#pragma unroll
+  for (int n = 0; n < NDMA; ++n) {
+    const int j = n * 512 + tid;
+    st8(Q0 + j * 8, zero8()); st8(G0 + j * 8, zero8());
+    st8(Q1 + j * 8, zero8()); st8(G1 + j * 8, zero8());
+    st8(Q2 + j * 8, zero8()); st8(G2 + j * 8, zero8());
+  }
+  __syncthreads();
+
+  // query tiles: G * n_self causal tiles (rows from key0 to the chunk end, for
+  // every head of the group), then the expert's packed rows
+  const int self_begin = key0;
+  const int n_self = (max(0, c_hi - self_begin) + kRows - 1) / kRows;
+  const int e = (f >= 0 && a.R > 0) ? f * a.Hkv + kh : -1;
+  const int n_rem = e >= 0 ? a.counts[e] : 0;
+  const int rbase = e >= 0 ? a.row_off[e] : 0;
+  const int n_tiles = G * n_self + (n_rem + kRows - 1) / kRows;
+  // row split: workgroup y of gridDim.y takes a contiguous share of the tiles
+  const int it_lo = (int)((int64_t)n_tiles * blockIdx.y / gridDim.y);
+  const int it_hi = (int)((int64_t)n_tiles * (blockIdx.y + 1) / gridDim.y);
+
+  // Tile loads: self tiles read q / dO / lse2 / delta in place (row stride
+  // Hq), expert tiles the packed copies (row stride 1); rows past the tile's
+  // valid range read past num_records, i.e. zeros, and a zero Q and dO row
+  // adds nothing.  Thread t loads blocks n * 512 + t; wave w loads lse2 and
+  // delta of rows 8w .. 8w + 7.
+  const uint32_t qbytes = (uint32_t)((int64_t)a.T * a.Hq * D * 2);
+  const uint32_t pbytes = (uint32_t)((int64_t)a.pack_rows * D * 2);
+  const uint32_t lbytes = (uint32_t)((int64_t)a.T * a.Hq * 4);
+  const uint32_t plbytes = (uint32_t)((int64_t)a.pack_rows * 4);
+  int jrow[NDMA], jcol[NDMA];
+#pragma unroll
+  for (int n = 0; n < NDMA; ++n) {
+    const int j = n * 512 + tid, q = j / NB;
+    jrow[n] = q;
+    jcol[n] = swz<DP>(q, (j % NB) * 8) - q * DP;
+  }
+  auto dma = [&](uint16_t* Qd, uint16_t* Gd, float* Ld, int it) __attribute__((always_inline)) {
+    const bool is_self = it < G * n_self;
+    int r0 = 0, rstride = 1, nvalid = 0;
+    if (it >= it_hi) {
+    } else if (is_self) {
+      const int g = it / n_self, s0 = self_begin + (it % n_self) * kRows;
+      r0 = s0 * a.Hq + kh * G + g; rstride = a.Hq; nvalid = min(kRows, c_hi - s0);
+    } else {
+      const int t = it - G * n_self;
+      r0 = rbase + t * kRows; rstride = 1; nvalid = min(kRows, n_rem - t * kRows);
+    }
+    const uint16_t* srcq = is_self ? a.q : a.pack_q;
+    const uint16_t* srcg = is_self ? a.dout : a.pack_g;
+    const uint32_t nb = is_self ? qbytes : pbytes;
+#pragma unroll
+    for (int n = 0; n < NDMA; ++n) {
+      const int q = jrow[n], col = jcol[n];
+      const uint32_t off = (q < nvalid && col < D)
+                               ? (uint32_t)(((int64_t)(r0 + q * rstride) * D + col) * 2) : nb;
+      const int jb = n * 512 + wave_s * 64;   // first block of this wave's 64
+      dma_lds16(make_rsrc(srcq, nb), Qd + jb * 8, off, 0);
+      dma_lds16(make_rsrc(srcg, nb), Gd + jb * 8, off, 0);
+    }
+    if (lane < 8) {
+      const int q = wave_s * 8 + lane;
+      const uint32_t lb = is_self ? lbytes : plbytes;
+      const uint32_t off = q < nvalid ? (uint32_t)(r0 + q * rstride) * 4 : lb;
+      dma_lds4(make_rsrc(is_self ? a.lse2 : a.pack_lse2, lb), Ld + wave_s * 8, off, 0);
+      dma_lds4(make_rsrc(is_self ? a.delta : a.pack_delta, lb), Ld + kRows + wave_s * 8, off, 0);
+    }
+  };
+
+  const uint32_t kq0 = swz_b128_base<DP>(lane);
+  const uint32_t trb0 = swz_tr_base<DP>(lane, 0), trb1 = swz_tr_base<DP>(lane, 1);
+  const float c2 = a.scale_log2;
+
+  // causal rows that end before the pair's first key contribute nothing
+  auto skipped = [&](int it) __attribute__((always_inline)) {
+    return it < G * n_self && self_begin + (it % n_self) * kRows + kRows - 1 < pkey0;
+  };
+  // A-operand rows (Q or dO) against the pair's K or V columns: 2 QB blocks
+  // of 32 rows x 32 keys, operand reads six steps ahead of the MFMAs
+  auto rows_x_keys = [&](const uint16_t* A, const u16x8_t (&kv)[NKS], f32x16_t (&sp)[QB])
+      __attribute__((always_inline)) {
+    const uint32_t kq = opaque(kq0);
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) sp[qb] = zero16();
+    constexpr int N1 = NKS * QB, PF = 6;
+    u16x8_t ring[PF];
+    auto rd = [&](int i) __attribute__((always_inline)) {
+      return lds8(A, (i % QB) * 32 * DP * 2 + swz_b128<DP>(kq, i / QB));
+    };
+#pragma unroll
+    for (int i = 0; i < PF && i < N1; ++i) ring[i] = rd(i);
+#pragma unroll
+    for (int i = 0; i < N1; ++i) {
+      const u16x8_t x = ring[i % PF];
+      if (i + PF < N1) ring[i % PF] = rd(i + PF);
+      sp[i % QB] = mfma32<DT>(x, kv[i / QB], sp[i % QB]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // acc (keys x d) += op^T B where B = transposed reads of a row-major tile
+  auto keys_x_d = [&](const uint16_t* B, const u16x8_t (&op)[QB][2], f32x16_t (&acc)[NDB])
+      __attribute__((always_inline)) {
+    const uint32_t t0 = opaque(trb0), t1 = opaque(trb1);
+    constexpr int N2 = NDB * QB * 2, PF = 6;
+    u16x8_t ring[PF];
+    // step i: d block i / (2 QB), row block (i / 2) % QB, half i % 2
+    auto rd = [&](int i) __attribute__((always_inline)) {
+      const uint32_t ro = (((i / 2) % QB) * 32 + (i % 2) * 16) * DP * 2;
+      const int db = i / (2 * QB);
+      return lds_tr8(B, ro + swz_tr<DP>(t0, db), ro + swz_tr<DP>(t1, db));
+    };
+#pragma unroll
+    for (int i = 0; i < PF && i < N2; ++i) ring[i] = rd(i);
+#pragma unroll
+    for (int i = 0; i < N2; ++i) {
+      const u16x8_t b = ring[i % PF];
+      if (i + PF < N2) ring[i % PF] = rd(i + PF);
+      acc[i / (2 * QB)] = mfma32<DT>(op[(i / 2) % QB][i % 2], b, acc[i / (2 * QB)]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  auto body = [&](auto role_tag) __attribute__((always_inline)) {
+    constexpr bool ROLE_P = decltype(role_tag)::value;
+    // K (role P) or V (role D) rows: B operands, column = key, k = d
+    u16x8_t kv[NKS];
+    const uint16_t* kvsrc = ROLE_P ? a.k : a.v;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const int d = ks * 16 + hh * 8;
+      kv[ks] = (mykey < c_hi && d < D) ? ld8(kvsrc + ((int64_t)mykey * a.Hkv + kh) * D + d) : zero8();
+    }
+    // the rows must have landed before the tile loads start: the compiler's
+    // own waits for them would otherwise also drain the tile loads in flight
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    f32x16_t acc[NDB];                          // dV (role P) or dK (role D)
+#pragma unroll
+    for (int i = 0; i < NDB; ++i) acc[i] = zero16();
+    f32x16_t dpl[QB];                           // role D: dP of the previous tile
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) dpl[qb] = zero16();
+
+    // role P at tile it (stage Qc, Gc, Lc)
+    auto p_step = [&](const uint16_t* Qc, const uint16_t* Gc, const float* Lc, int it)
+        __attribute__((always_inline)) {
+      if (it >= it_hi || skipped(it)) return;
+      const bool is_self = it < G * n_self;
+      const int sq0 = is_self ? self_begin + (it % n_self) * kRows : 0;
+      const bool need_mask = (pkey0 + kPairKeys > c_hi) || (is_self && sq0 < pkey0 + kPairKeys - 1);
+      f32x16_t sp[QB];
+      rows_x_keys(Qc, kv, sp);
+      u16x8_t pk[QB][2];
+      auto to_p = [&](auto mask_tag) __attribute__((always_inline)) {
+        constexpr bool MASK = decltype(mask_tag)::value;
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int r0 = qb * 32 + 8 * j + 4 * hh;
+            const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(Lc + r0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              float p = fast_exp2(fmaf(sp[qb][4 * j + i], c2, -l4[i]));
+              if constexpr (MASK) p = (mykey < c_hi && (!is_self || mykey <= sq0 + r0 + i)) ? p : 0.0f;
+              pk[qb][j >> 1][(j & 1) * 4 + i] = from_f32<DT>(p);
+            }
+          }
+      };
+      if (need_mask) to_p(std::true_type{}); else to_p(std::false_type{});
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        Px[it & 1][pair][qb][0][lane] = pk[qb][0];
+        Px[it & 1][pair][qb][1][lane] = pk[qb][1];
+      }
+      keys_x_d(Gc, pk, acc);
+    };
+    // role D: dS / dK of tile it - 1 (stage Qp, Lp), then dP of tile it (Gc)
+    auto d_prev = [&](const uint16_t* Qp, const float* Lp, int itp) __attribute__((always_inline)) {
+      if (itp < it_lo || skipped(itp)) return;
+      u16x8_t op[QB][2];
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        const u16x8_t px[2] = {Px[itp & 1][pair][qb][0][lane], Px[itp & 1][pair][qb][1][lane]};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(Lp + kRows + qb * 32 + 8 * j + 4 * hh);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = 4 * j + i, h2 = j >> 1, x = (j & 1) * 4 + i;
+            op[qb][h2][x] = from_f32<DT>(to_f32<DT>(px[h2][x]) * (dpl[qb][r] - d4[i]));
+          }
+        }
+      }
+      keys_x_d(Qp, op, acc);
+    };
+    auto d_cur = [&](const uint16_t* Gc, int it) __attribute__((always_inline)) {
+      if (it >= it_hi || skipped(it)) return;
+      rows_x_keys(Gc, kv, dpl);
+    };
+    // one tile: stage c holds tile it, stage p tile it - 1, stage n receives
+    // tile it + 1; afterwards this wave's loads of tile it + 1 have landed and
+    // the barrier makes every wave's loads and P writes visible
+    auto step = [&](uint16_t* Qp, uint16_t* Gp, float* Lp, uint16_t* Qc, uint16_t* Gc, float* Lc,
+                    uint16_t* Qn, uint16_t* Gn, float* Ln, int it) __attribute__((always_inline)) {
+      dma(Qn, Gn, Ln, it + 1);
+      if constexpr (ROLE_P) {
+        p_step(Qc, Gc, Lc, it);
+      } else {
+        d_prev(Qp, Lp, it - 1);
+        d_cur(Gc, it);
+      }
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      lds_barrier();
+    };
+    dma(Q0, G0, L0, it_lo);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    lds_barrier();
+    // stages rotate with period 3: tile it lives in stage (it - it_lo) % 3;
+    // the loop runs one step past it_hi so role D finishes the last tile
+    for (int it = it_lo; it <= it_hi; it += 3) {
+      step(Q2, G2, L2, Q0, G0, L0, Q1, G1, L1, it);
+      if (it + 1 > it_hi) break;
+      step(Q0, G0, L0, Q1, G1, L1, Q2, G2, L2, it + 1);
+      if (it + 2 > it_hi) break;
+      step(Q1, G1, L1, Q2, G2, L2, Q0, G0, L0, it + 2);
+    }
+
+    // D layout: lane holds column d = i*32 + qi, keys 8j + 4hh + r.  With a
+    // row split the fp32 partials go to part_dkv[(split, dk|dv)] for the
+    // fixed-order reduction.
+    const int64_t nkd = (int64_t)a.T * a.Hkv * D;
+    float* pdst = a.part_dkv + ((int64_t)blockIdx.y * 2 + (ROLE_P ? 1 : 0)) * nkd;
+    uint16_t* dst = ROLE_P ? a.dv : a.dk;
+    const float osc = ROLE_P ? 1.0f : a.scale;
+#pragma unroll
+    for (int i = 0; i < NDB; ++i) {
+      const int d = i * 32 + qi;
+      if (d >= D) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = pkey0 + 8 * (r >> 2) + 4 * hh + (r & 3);
+        if (key >= c_hi) continue;
+        const int64_t o = ((int64_t)key * a.Hkv + kh) * D + d;
+        if (gridDim.y > 1) pdst[o] = acc[i][r];
+        else dst[o] = from_f32<DT>(acc[i][r] * osc);
+      }
+    }
+  };
+  if (role_p) body(std::true_type{}); else body(std::false_type{});
+}
+
+}  // namespace
+
+template <int DT, int DP> void launch_dkdv2(const BwdArgs& a, int n_kv, hipStream_t st) {
+  hipLaunchKernelGGL((dkdv2_kernel<DT, DP>), dim3(n_kv, a.kv_splits), dim3(512), 0, st, a);
+}
+
+template void launch_dkdv2<0, 128>(const BwdArgs&, int, hipStream_t);
+template void launch_dkdv2<1, 128>(const BwdArgs&, int, hipStream_t);
+
+}  // namespace moba

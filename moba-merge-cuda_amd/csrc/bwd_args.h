@@ -45,5 +45,6 @@ struct BwdArgs {
 // Key-major dK/dV with all four products per wave (attn_dkdv.hip), head dims <= 64:
 // launches the kernel over n_kv key tiles of 128 keys x kv_splits row splits.
 template <int DT, int DP> void launch_dkdv1(const BwdArgs& a, int n_kv, hipStream_t st);
+template <int DT, int DP> void launch_dkdv2(const BwdArgs& a, int n_kv, hipStream_t st);
 
 }  // namespace moba

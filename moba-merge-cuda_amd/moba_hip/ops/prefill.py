@@ -236,7 +236,7 @@ def backward(plan: PrefillPlan, q, k, v, out, lse, dout, rt: RouteResult | None)
                 if ks > 1 else None)
     # expert rows of q / dO / lse / delta packed contiguously for the key-major kernel
     pack = (torch.empty(T * hq * R * (4 * d + 8), dtype=torch.uint8, device=dev)
-            if R and d <= 64 else None)
+            if R and d <= 128 else None)
     st = _lib.stream_of(dev)
     _lib.call("moba_hip_prefill_bwd", *args, 1, ks, _lib.ptr(part_dkv), None, st)
     events = DKDV_EVENTS
