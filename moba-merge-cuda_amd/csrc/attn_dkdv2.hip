@@ -12,18 +12,22 @@
 //
 // A workgroup of 8 waves owns 128 keys of one chunk and one KV head as 4 wave
 // pairs of 32 keys; the two waves of a pair share a SIMD.  For 64-row tiles
-// of (Q, dO) rows:
-//   role P (K in registers, dV accumulators), at tile i:
-//       S = Q_i K^T, P = exp2(S*c - lse2) -> LDS (input dtype), dV += P^T dO_i
-//   role D (V in registers, dK accumulators), at tile i:
-//       dS_{i-1} = P_{i-1} (dP_{i-1} - delta), dK += dS^T Q_{i-1}  (P from LDS)
-//       dP_i = dO_i V^T                        (kept in registers for i + 1)
-// Role D runs one tile behind role P on the P it needs, so the only
-// synchronisation is the barrier where the LDS stages rotate: P_{i-1} was
-// written before it.  Three stages hold tiles i - 1 (role D's Q), i and
-// i + 1 (loading).  The expert rows come packed contiguously (pack_rows_kernel),
-// so every tile is affine in the row number and is loaded HBM -> LDS by
-// buffer loads issued from inline assembly (the waits are placed here).
+// of (Q, dO) rows, at step t:
+//   role P (K in registers, dV accumulators):
+//       one MFMA block: S_t = Q_t K^T  interleaved with  dV += P_{t-1}^T dO_{t-1}
+//       then P_t = exp2(S_t*c - lse2) -> registers and LDS (input dtype)
+//   role D (V in registers, dK accumulators):
+//       dS_{t-1} = P_{t-1} (dP_{t-1} - delta)          (P from LDS)
+//       then one MFMA block: dK += dS_{t-1}^T Q_{t-1}  interleaved with  dP_t = dO_t V^T
+// Each role alternates a VALU phase and an MFMA block of two independent
+// accumulator chains, in opposite order, so the SIMD's MFMA unit is fed by
+// one wave while the other does its element-wise work.  Role D runs one tile
+// behind role P on the P it needs, so the only synchronisation is the
+// barrier where the LDS stages rotate: P_{t-1} was written before it.  Three
+// stages hold tiles t - 1, t and t + 1 (loading).  The expert rows come
+// packed contiguously (pack_rows_kernel), so every tile is affine in the row
+// number and is loaded HBM -> LDS by buffer loads issued from inline
+// assembly (the waits are placed here).
 #include <type_traits>
 
 #include "common.h"
@@ -107,16 +111,26 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
     jrow[n] = q;
     jcol[n] = swz<DP>(q, (j % NB) * 8) - q * DP;
   }
-  auto dma = [&](uint16_t* Qd, uint16_t* Gd, float* Ld, int it) __attribute__((always_inline)) {
-    const bool is_self = it < G * n_self;
+  // Tile cursor: tile `it` is causal tile s of head g while g < G, else
+  // expert tile s; advanced by one per step (no divisions in the loop).
+  struct Cur { int it, g, s; };
+  auto cur_at = [&](int it) __attribute__((always_inline)) {
+    return it < G * n_self ? Cur{it, it / n_self, it % n_self} : Cur{it, G, it - G * n_self};
+  };
+  auto cur_next = [&](Cur t) __attribute__((always_inline)) {
+    ++t.it; ++t.s;
+    if (t.g < G && t.s == n_self) { t.s = 0; ++t.g; }
+    return t;
+  };
+  auto dma = [&](uint16_t* Qd, uint16_t* Gd, float* Ld, Cur t) __attribute__((always_inline)) {
+    const bool is_self = t.g < G;
     int r0 = 0, rstride = 1, nvalid = 0;
-    if (it >= it_hi) {
+    if (t.it >= it_hi) {
     } else if (is_self) {
-      const int g = it / n_self, s0 = self_begin + (it % n_self) * kRows;
-      r0 = s0 * a.Hq + kh * G + g; rstride = a.Hq; nvalid = min(kRows, c_hi - s0);
+      const int s0 = self_begin + t.s * kRows;
+      r0 = s0 * a.Hq + kh * G + t.g; rstride = a.Hq; nvalid = min(kRows, c_hi - s0);
     } else {
-      const int t = it - G * n_self;
-      r0 = rbase + t * kRows; rstride = 1; nvalid = min(kRows, n_rem - t * kRows);
+      r0 = rbase + t.s * kRows; rstride = 1; nvalid = min(kRows, n_rem - t.s * kRows);
     }
     const uint16_t* srcq = is_self ? a.q : a.pack_q;
     const uint16_t* srcg = is_self ? a.dout : a.pack_g;
@@ -144,52 +158,65 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
   const float c2 = a.scale_log2;
 
   // causal rows that end before the pair's first key contribute nothing
-  auto skipped = [&](int it) __attribute__((always_inline)) {
-    return it < G * n_self && self_begin + (it % n_self) * kRows + kRows - 1 < pkey0;
+  auto skipped = [&](Cur t) __attribute__((always_inline)) {
+    return t.g < G && t.s * kRows + kRows - 1 < pair * kPairKeys;
   };
-  // A-operand rows (Q or dO) against the pair's K or V columns: 2 QB blocks
-  // of 32 rows x 32 keys, operand reads six steps ahead of the MFMAs
-  auto rows_x_keys = [&](const uint16_t* A, const u16x8_t (&kv)[NKS], f32x16_t (&sp)[QB])
-      __attribute__((always_inline)) {
-    const uint32_t kq = opaque(kq0);
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) sp[qb] = zero16();
-    constexpr int N1 = NKS * QB, PF = 6;
-    u16x8_t ring[PF];
-    auto rd = [&](int i) __attribute__((always_inline)) {
+  // One MFMA block of up to two independent chains, interleaved step by
+  // step, each with its operand reads PF steps ahead (PF = 3 when both run):
+  //   chain A: sp (rows x keys) = A (rows, b128 reads) x kv (keys in registers)
+  //   chain B: acc (keys x d) += op^T (in registers) x B (rows, transposed reads)
+  // Both chains are NKS * QB = NDB * QB * 2 MFMAs long.
+  auto block = [&](auto da_tag, auto db_tag, const uint16_t* A, const u16x8_t (&kv)[NKS],
+                   f32x16_t (&sp)[QB], const uint16_t* B, const u16x8_t (&op)[QB][2],
+                   f32x16_t (&acc)[NDB]) __attribute__((always_inline)) {
+    constexpr bool DA = decltype(da_tag)::value, DB = decltype(db_tag)::value;
+    constexpr int N = NKS * QB, PF = (DA && DB) ? 3 : 6;
+    static_assert(N == NDB * QB * 2, "chain lengths");
+    const uint32_t kq = opaque(kq0), t0 = opaque(trb0), t1 = opaque(trb1);
+    // chain A step i: row block i % QB, k block i / QB
+    auto rda = [&](int i) __attribute__((always_inline)) {
       return lds8(A, (i % QB) * 32 * DP * 2 + swz_b128<DP>(kq, i / QB));
     };
+    // chain B step i: d block i % NDB, row block (i / NDB / 2) % QB, half (i / NDB) % 2
+    // (consecutive steps feed different accumulators)
+    auto rdb = [&](int i) __attribute__((always_inline)) {
+      const int j = i / NDB;
+      const uint32_t ro = (((j / 2) % QB) * 32 + (j % 2) * 16) * DP * 2;
+      return lds_tr8(B, ro + swz_tr<DP>(t0, i % NDB), ro + swz_tr<DP>(t1, i % NDB));
+    };
+    u16x8_t ra[PF], rb[PF];
+    if constexpr (DA) {
 #pragma unroll
-    for (int i = 0; i < PF && i < N1; ++i) ring[i] = rd(i);
+      for (int qb = 0; qb < QB; ++qb) sp[qb] = zero16();
+    }
 #pragma unroll
-    for (int i = 0; i < N1; ++i) {
-      const u16x8_t x = ring[i % PF];
-      if (i + PF < N1) ring[i % PF] = rd(i + PF);
-      sp[i % QB] = mfma32<DT>(x, kv[i / QB], sp[i % QB]);
-      __builtin_amdgcn_sched_barrier(0);
+    for (int i = 0; i < PF; ++i) {
+      if constexpr (DA) ra[i] = rda(i);
+      if constexpr (DB) rb[i] = rdb(i);
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      if constexpr (DA) {
+        const u16x8_t x = ra[i % PF];
+        if (i + PF < N) ra[i % PF] = rda(i + PF);
+        sp[i % QB] = mfma32<DT>(x, kv[i / QB], sp[i % QB]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if constexpr (DB) {
+        const u16x8_t b = rb[i % PF];
+        if (i + PF < N) rb[i % PF] = rdb(i + PF);
+        acc[i % NDB] = mfma32<DT>(op[(i / NDB / 2) % QB][(i / NDB) % 2], b, acc[i % NDB]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
   };
-  // acc (keys x d) += op^T B where B = transposed reads of a row-major tile
-  auto keys_x_d = [&](const uint16_t* B, const u16x8_t (&op)[QB][2], f32x16_t (&acc)[NDB])
-      __attribute__((always_inline)) {
-    const uint32_t t0 = opaque(trb0), t1 = opaque(trb1);
-    constexpr int N2 = NDB * QB * 2, PF = 6;
-    u16x8_t ring[PF];
-    // step i: d block i / (2 QB), row block (i / 2) % QB, half i % 2
-    auto rd = [&](int i) __attribute__((always_inline)) {
-      const uint32_t ro = (((i / 2) % QB) * 32 + (i % 2) * 16) * DP * 2;
-      const int db = i / (2 * QB);
-      return lds_tr8(B, ro + swz_tr<DP>(t0, db), ro + swz_tr<DP>(t1, db));
-    };
-#pragma unroll
-    for (int i = 0; i < PF && i < N2; ++i) ring[i] = rd(i);
-#pragma unroll
-    for (int i = 0; i < N2; ++i) {
-      const u16x8_t b = ring[i % PF];
-      if (i + PF < N2) ring[i % PF] = rd(i + PF);
-      acc[i / (2 * QB)] = mfma32<DT>(op[(i / 2) % QB][i % 2], b, acc[i / (2 * QB)]);
-      __builtin_amdgcn_sched_barrier(0);
-    }
+  // the block for runtime flags (chain A: current tile, chain B: previous tile)
+  auto run_block = [&](bool cur, bool prev, const uint16_t* A, const u16x8_t (&kv)[NKS],
+                       f32x16_t (&sp)[QB], const uint16_t* B, const u16x8_t (&op)[QB][2],
+                       f32x16_t (&acc)[NDB]) __attribute__((always_inline)) {
+    if (cur && prev) block(std::true_type{}, std::true_type{}, A, kv, sp, B, op, acc);
+    else if (cur) block(std::true_type{}, std::false_type{}, A, kv, sp, B, op, acc);
+    else if (prev) block(std::false_type{}, std::true_type{}, A, kv, sp, B, op, acc);
   };
 
   auto body = [&](auto role_tag) __attribute__((always_inline)) {
@@ -208,20 +235,24 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
     f32x16_t acc[NDB];                          // dV (role P) or dK (role D)
 #pragma unroll
     for (int i = 0; i < NDB; ++i) acc[i] = zero16();
-    f32x16_t dpl[QB];                           // role D: dP of the previous tile
+    // role P: S of the current tile; role D: dP of the last computed tile
+    f32x16_t sp[QB];
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) dpl[qb] = zero16();
+    for (int qb = 0; qb < QB; ++qb) sp[qb] = zero16();
+    // role P: P of the previous tile; role D: dS of the previous tile
+    u16x8_t op[QB][2];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) op[qb][0] = op[qb][1] = zero8();
 
-    // role P at tile it (stage Qc, Gc, Lc)
-    auto p_step = [&](const uint16_t* Qc, const uint16_t* Gc, const float* Lc, int it)
-        __attribute__((always_inline)) {
-      if (it >= it_hi || skipped(it)) return;
-      const bool is_self = it < G * n_self;
-      const int sq0 = is_self ? self_begin + (it % n_self) * kRows : 0;
+    // role P, tile t in stage (Qc, Lc), previous tile's dO in Gp:
+    //   S_t and dV += P_prev^T dO_prev in one block, then P_t -> op and LDS
+    auto p_step = [&](const uint16_t* Qc, const float* Lc, const uint16_t* Gp, Cur t, bool cur,
+                      bool prev) __attribute__((always_inline)) {
+      run_block(cur, prev, Qc, kv, sp, Gp, op, acc);
+      if (!cur) return;
+      const bool is_self = t.g < G;
+      const int sq0 = is_self ? self_begin + t.s * kRows : 0;
       const bool need_mask = (pkey0 + kPairKeys > c_hi) || (is_self && sq0 < pkey0 + kPairKeys - 1);
-      f32x16_t sp[QB];
-      rows_x_keys(Qc, kv, sp);
-      u16x8_t pk[QB][2];
       auto to_p = [&](auto mask_tag) __attribute__((always_inline)) {
         constexpr bool MASK = decltype(mask_tag)::value;
 #pragma unroll
@@ -234,67 +265,68 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
             for (int i = 0; i < 4; ++i) {
               float p = fast_exp2(fmaf(sp[qb][4 * j + i], c2, -l4[i]));
               if constexpr (MASK) p = (mykey < c_hi && (!is_self || mykey <= sq0 + r0 + i)) ? p : 0.0f;
-              pk[qb][j >> 1][(j & 1) * 4 + i] = from_f32<DT>(p);
+              op[qb][j >> 1][(j & 1) * 4 + i] = from_f32<DT>(p);
             }
           }
       };
       if (need_mask) to_p(std::true_type{}); else to_p(std::false_type{});
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
-        Px[it & 1][pair][qb][0][lane] = pk[qb][0];
-        Px[it & 1][pair][qb][1][lane] = pk[qb][1];
+        Px[t.it & 1][pair][qb][0][lane] = op[qb][0];
+        Px[t.it & 1][pair][qb][1][lane] = op[qb][1];
       }
-      keys_x_d(Gc, pk, acc);
     };
-    // role D: dS / dK of tile it - 1 (stage Qp, Lp), then dP of tile it (Gc)
-    auto d_prev = [&](const uint16_t* Qp, const float* Lp, int itp) __attribute__((always_inline)) {
-      if (itp < it_lo || skipped(itp)) return;
-      u16x8_t op[QB][2];
+    // role D: dS_prev = P_prev (dP_prev - delta) from LDS and registers, then
+    // dK += dS_prev^T Q_prev and dP_t = dO_t V^T in one block
+    auto d_step = [&](const uint16_t* Gc, const uint16_t* Qp, const float* Lp, Cur t, bool cur,
+                      bool prev) __attribute__((always_inline)) {
+      if (prev) {
+        const int b = (t.it - 1) & 1;
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) {
-        const u16x8_t px[2] = {Px[itp & 1][pair][qb][0][lane], Px[itp & 1][pair][qb][1][lane]};
+        for (int qb = 0; qb < QB; ++qb) {
+          const u16x8_t px[2] = {Px[b][pair][qb][0][lane], Px[b][pair][qb][1][lane]};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(Lp + kRows + qb * 32 + 8 * j + 4 * hh);
+          for (int j = 0; j < 4; ++j) {
+            const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(Lp + kRows + qb * 32 + 8 * j + 4 * hh);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int r = 4 * j + i, h2 = j >> 1, x = (j & 1) * 4 + i;
-            op[qb][h2][x] = from_f32<DT>(to_f32<DT>(px[h2][x]) * (dpl[qb][r] - d4[i]));
+            for (int i = 0; i < 4; ++i) {
+              const int r = 4 * j + i, h2 = j >> 1, x = (j & 1) * 4 + i;
+              op[qb][h2][x] = from_f32<DT>(to_f32<DT>(px[h2][x]) * (sp[qb][r] - d4[i]));
+            }
           }
         }
       }
-      keys_x_d(Qp, op, acc);
+      run_block(cur, prev, Gc, kv, sp, Qp, op, acc);
     };
-    auto d_cur = [&](const uint16_t* Gc, int it) __attribute__((always_inline)) {
-      if (it >= it_hi || skipped(it)) return;
-      rows_x_keys(Gc, kv, dpl);
-    };
-    // one tile: stage c holds tile it, stage p tile it - 1, stage n receives
-    // tile it + 1; afterwards this wave's loads of tile it + 1 have landed and
-    // the barrier makes every wave's loads and P writes visible
+    // one tile: stage c holds tile tc, stage p the tile before (computed when
+    // pv), stage n receives the next tile; afterwards this wave's loads of
+    // the next tile have landed and the barrier makes every wave's loads and
+    // P writes visible
+    Cur tc = cur_at(it_lo);
+    bool pv = false;
     auto step = [&](uint16_t* Qp, uint16_t* Gp, float* Lp, uint16_t* Qc, uint16_t* Gc, float* Lc,
-                    uint16_t* Qn, uint16_t* Gn, float* Ln, int it) __attribute__((always_inline)) {
-      dma(Qn, Gn, Ln, it + 1);
-      if constexpr (ROLE_P) {
-        p_step(Qc, Gc, Lc, it);
-      } else {
-        d_prev(Qp, Lp, it - 1);
-        d_cur(Gc, it);
-      }
+                    uint16_t* Qn, uint16_t* Gn, float* Ln) __attribute__((always_inline)) {
+      const Cur tn = cur_next(tc);
+      dma(Qn, Gn, Ln, tn);
+      const bool cur = tc.it < it_hi && !skipped(tc);
+      if constexpr (ROLE_P) p_step(Qc, Lc, Gp, tc, cur, pv);
+      else d_step(Gc, Qp, Lp, tc, cur, pv);
+      pv = cur;
+      tc = tn;
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
       lds_barrier();
     };
-    dma(Q0, G0, L0, it_lo);
+    dma(Q0, G0, L0, tc);
     __builtin_amdgcn_s_waitcnt(0x0F70);
     lds_barrier();
     // stages rotate with period 3: tile it lives in stage (it - it_lo) % 3;
-    // the loop runs one step past it_hi so role D finishes the last tile
+    // the loop runs one step past it_hi so both roles finish the last tile
     for (int it = it_lo; it <= it_hi; it += 3) {
-      step(Q2, G2, L2, Q0, G0, L0, Q1, G1, L1, it);
+      step(Q2, G2, L2, Q0, G0, L0, Q1, G1, L1);
       if (it + 1 > it_hi) break;
-      step(Q0, G0, L0, Q1, G1, L1, Q2, G2, L2, it + 1);
+      step(Q0, G0, L0, Q1, G1, L1, Q2, G2, L2);
       if (it + 2 > it_hi) break;
-      step(Q1, G1, L1, Q2, G2, L2, Q0, G0, L0, it + 2);
+      step(Q1, G1, L1, Q2, G2, L2, Q0, G0, L0);
     }
 
     // D layout: lane holds column d = i*32 + qi, keys 8j + 4hh + r.  With a
