@@ -317,7 +317,7 @@ def main():
                        "entry": "moba_hip.run_impl('opt_hip')", "seq_len": 32768},
             "mfma_frac": round(res3["mfma_frac"], 4),
             "tflops": round(res3["tflops"], 1),
-            "roofline": {"bound": "mfma", "kernel": "dkdv_kernel<bf16,128>",
+            "roofline": {"bound": "mfma", "kernel": "dkdv2_kernel<bf16,128>",
                          "achieved": round(ach, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(ach / BF16_PEAK_TFLOPS, 4), "traffic": traffic,
                          "traffic_unit": "bytes per launch (profiles/dkdv_cfg3_traffic.md)",

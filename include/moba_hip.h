@@ -96,11 +96,14 @@ int moba_hip_prefill_fwd(const void* q, const void* k, const void* v, int dtype,
  * filtered index or -1, kv head): one workgroup per entry, tiles of 128
  * keys; chunk -1 marks an empty entry.  delta [2*T*Hq] and
  * part_dq [T*Hq*R, D] fp32 are workspaces.  pack is a workspace of
- * T*Hq*R*(4*D + 8) bytes for parts & 2 when R > 0 and D <= 128 (the expert
- * rows of q, dO, lse and delta copied contiguously), else may be NULL.  dq [T,Hq,D], dk/dv [T,Hkv,D]
- * (dtype) are fully written (every key belongs to exactly one kv tile).
- * parts selects the launches: 1 = Delta and dq (query-major kernels), 2 = dk/dv
- * (key-major kernel, needs the Delta of a parts-1 call), 3 = both in order.
+ * T*Hq*R*(4*D + 8) bytes, required when R > 0 and D <= 128 (the expert rows
+ * of q, dO, lse and delta copied contiguously by the parts-1 launches and read
+ * by the key-major kernel: pass the same buffer to both calls), else may be
+ * NULL.  dq [T,Hq,D], dk/dv [T,Hkv,D] (dtype) are fully written (every key
+ * belongs to exactly one kv tile).
+ * parts selects the launches: 1 = Delta, expert-row packing and dq
+ * (query-major kernels), 2 = dk/dv (key-major kernel, needs the Delta and
+ * packing of a parts-1 call), 3 = both in order.
  * kv_splits in [1,16]: each key tile's query rows are split over that many
  * workgroups (for few kv heads); when > 1, part_dkv [kv_splits*2*T*Hkv*D]
  * fp32 is a workspace and D must be a multiple of 8.

@@ -727,6 +727,10 @@ int launch_bwd(const BwdArgs& a, int n_self, int n_kv, int max_remote, int parts
   if (parts & 1) {
     hipLaunchKernelGGL(delta_kernel<DT>, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, st,
                        a.out, a.dout, a.lse, rows, a.D, a.delta, a.lse2);
+    if (DP <= 128 && a.pack_rows > 0) {  // expert rows for the key-major kernel
+      const int64_t pieces = a.pack_rows * (a.D / 8);
+      hipLaunchKernelGGL(pack_rows_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, st, a);
+    }
     if (max_remote > 0 && a.R > 0)
       hipLaunchKernelGGL((dq_kernel<DT, DP, true, attn_qb<DP>()>), dim3((max_remote + 7) / 8 * 8), dim3(256), 0, st, a);
     if (n_self > 0)
@@ -735,10 +739,6 @@ int launch_bwd(const BwdArgs& a, int n_self, int n_kv, int max_remote, int parts
   if ((parts & 2) && n_kv > 0) {
     // 128 keys per workgroup in both kernels; the host's key tiles match
     if constexpr (DP <= 128) {
-      if (a.pack_rows > 0) {
-        const int64_t pieces = a.pack_rows * (a.D / 8);
-        hipLaunchKernelGGL(pack_rows_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, st, a);
-      }
       if constexpr (DP <= 64) launch_dkdv1<DT, DP>(a, n_kv, st);
       else launch_dkdv2<DT, DP>(a, n_kv, st);
     } else {
@@ -796,7 +796,7 @@ extern "C" int moba_hip_prefill_bwd(const void* q, const void* k, const void* v,
   a.pack_g = a.pack_q + a.pack_rows * D;
   a.pack_lse2 = (float*)(a.pack_g + a.pack_rows * D);
   a.pack_delta = a.pack_lse2 + a.pack_rows;
-  if (a.pack_rows > 0 && (parts & 2) && pack == nullptr) { moba_set_error("prefill_bwd: the pack workspace is required when R > 0 and head_dim <= 128"); return MOBA_ERR_ARG; }
+  if (a.pack_rows > 0 && pack == nullptr) { moba_set_error("prefill_bwd: the pack workspace is required when R > 0 and head_dim <= 128"); return MOBA_ERR_ARG; }
   if (a.pack_rows * D * 2 >= ((int64_t)1 << 32)) { moba_set_error("prefill_bwd: packed expert rows must be smaller than 4 GiB (32-bit buffer offsets)"); return MOBA_ERR_ARG; }
   hipStream_t st = (hipStream_t)stream;
   const int mr = R > 0 ? max_remote_tiles : 0;

@@ -238,7 +238,7 @@ def backward(plan: PrefillPlan, q, k, v, out, lse, dout, rt: RouteResult | None)
     pack = (torch.empty(T * hq * R * (4 * d + 8), dtype=torch.uint8, device=dev)
             if R and d <= 128 else None)
     st = _lib.stream_of(dev)
-    _lib.call("moba_hip_prefill_bwd", *args, 1, ks, _lib.ptr(part_dkv), None, st)
+    _lib.call("moba_hip_prefill_bwd", *args, 1, ks, _lib.ptr(part_dkv), _lib.ptr(pack), st)
     events = DKDV_EVENTS
     if events is not None:
         events[0].record()
