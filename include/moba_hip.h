@@ -19,6 +19,8 @@
 #ifndef MOBA_HIP_H
 #define MOBA_HIP_H
 
+#include <stdint.h>
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -64,11 +66,17 @@ int moba_hip_route_prefill(const void* q, int dtype, int T, int Hq, int Hkv, int
  * counts[E], row_off[E+1], tile_off[E+1] (tiles of block_rows rows), rows[sum
  * counts] = ((s*Hq + h) << 3) | j where j is the chunk's rank in sel[s,h,:]
  * (R <= 8, T*Hq < 2^28); the partial slot of that row is (s*Hq + h)*R + j.
+ * work is an int32 workspace of moba_hip_pack_experts_work(T, Hq, Hkv, F)
+ * entries (per-block candidate counts of each expert).
  * Replaces the nonzero/index_select packing of grouped_attention.py:78-94. */
 int moba_hip_pack_experts(const int* sel, int T, int Hq, int Hkv, int R,
                           const int* cu_chunk, const int* chunk_batch, const int* cu_seqlens,
                           const int* filtered, int F, int block_rows, int* counts,
-                          int* row_off, int* tile_off, int* rows, void* stream);
+                          int* row_off, int* tile_off, int* rows, int* work, void* stream);
+
+/* Size in int32 entries of the work buffer of moba_hip_pack_experts (-1 for a
+ * bad shape).  Helper of the entry above; no counterpart in the reference. */
+int64_t moba_hip_pack_experts_work(int T, int Hq, int Hkv, int F);
 
 /* Sparse block attention forward + global-softmax merge.
  * Replaces OptMixedAttention.forward (src/moba_opt/mixed_attention.py:42-139):

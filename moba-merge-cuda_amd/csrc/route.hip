@@ -19,52 +19,80 @@ namespace {
 
 constexpr int kMaxRemote = 8;
 
-// One wave per (filtered chunk, kv head, 8 consecutive d): lane j sums the
-// tokens j, j+64, ... (16-byte loads), then the canonical tree.
-template <int DT>
-__global__ __launch_bounds__(64) void chunk_means_kernel(const uint16_t* __restrict__ k, int Hkv,
-                                                         int D, const int* __restrict__ chunk_start,
-                                                         int C, int precision,
-                                                         float* __restrict__ means) {
-  const int nd8 = D / 8;
-  const int db = blockIdx.x % nd8;
-  const int kh = (blockIdx.x / nd8) % Hkv;
-  const int f = blockIdx.x / (nd8 * Hkv);
-  const int lane = threadIdx.x;
-  const uint16_t* p = k + ((int64_t)chunk_start[f] * Hkv + kh) * D + db * 8;
+// One workgroup per (filtered chunk, kv head).  The mean of dim d is the
+// canonical sum: 64 partial sums s_j over the tokens j, j+64, j+128, ... in
+// increasing order, then the fixed tree canon_tree over j.  Work item
+// (j, column block b) of 8 dims is p = j * nd8 + b, so a wave's loads cover
+// whole rows (coalesced); thread t owns items t, t + 256, ...  The partials
+// go through LDS to one wave per dim, lane j holding s_j, for the tree.
+template <int DT, int NP>
+__global__ __launch_bounds__(256) void chunk_means_kernel(const uint16_t* __restrict__ k, int Hkv,
+                                                          int D, const int* __restrict__ chunk_start,
+                                                          int C, int precision,
+                                                          float* __restrict__ means) {
+  extern __shared__ float part[];  // [64][D]
+  const int nd8 = D / 8, np = 64 * nd8;
+  const int kh = blockIdx.x % Hkv, f = blockIdx.x / Hkv;
+  const int tid = threadIdx.x;
   const int64_t stride = (int64_t)Hkv * D;
-  float acc[8];
+  const uint16_t* base = k + ((int64_t)chunk_start[f] * Hkv + kh) * D;
+  float acc[NP][8];
+  int jj[NP], bb[NP];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
-  for (int t = lane; t < C; t += 64) {
-    const u16x8_t x = ld8(p + t * stride);
+  for (int i = 0; i < NP; ++i) {
+    const int p = tid + 256 * i;
+    jj[i] = p < np ? p / nd8 : C;  // items past np load nothing
+    bb[i] = p % nd8;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] = acc[e] + to_f32<DT>(x[e]);
+    for (int e = 0; e < 8; ++e) acc[i][e] = 0.0f;
   }
-  float out[8];
+  for (int t0 = 0; t0 < C; t0 += 64) {
+    u16x8_t x[NP];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    float m = canon_tree(acc[e]) / (float)C;
+    for (int i = 0; i < NP; ++i) {
+      const int t = t0 + jj[i];
+      x[i] = t < C ? ld8(base + t * stride + bb[i] * 8) : zero8();
+    }
+#pragma unroll
+    for (int i = 0; i < NP; ++i)
+      if (t0 + jj[i] < C) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[i][e] = acc[i][e] + to_f32<DT>(x[i][e]);
+      }
+  }
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const int p = tid + 256 * i;
+    if (p < np) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part[jj[i] * D + bb[i] * 8 + e] = acc[i][e];
+    }
+  }
+  __syncthreads();
+  const int lane = tid & 63, w = tid >> 6;
+  float* dst = means + ((int64_t)f * Hkv + kh) * D;
+  for (int d = w; d < D; d += 4) {
+    float m = canon_tree(part[lane * D + d]) / (float)C;
     if (precision == 0) m = to_f32<DT>(from_f32<DT>(m));
-    out[e] = m;
-  }
-  if (lane == 0) {
-    float* dst = means + ((int64_t)f * Hkv + kh) * D + db * 8;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) dst[e] = out[e];
+    if (lane == 0) dst[d] = m;
   }
 }
 
-// One thread per (token, q head); heads fastest so a wave reads adjacent q rows.
-template <int DT>
-__global__ void route_kernel(const uint16_t* __restrict__ q, int T, int Hq, int Hkv, int D,
-                             const float* __restrict__ means, const int* __restrict__ cu_chunk,
-                             int nchunk, const int* __restrict__ chunk_batch,
-                             const int* __restrict__ first_chunk, int R, int F,
-                             int* __restrict__ sel, float* __restrict__ gate) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (int64_t)T * Hq) return;
-  const int s = (int)(idx / Hq), h = (int)(idx % Hq);
+// One thread per (token, q head): a workgroup takes 256 consecutive tokens of
+// one head, so the means rows read in the candidate loop are the same for the
+// whole wave, and the token's q row is read once into registers.
+template <int DT, int DP>
+__global__ __launch_bounds__(256) void route_kernel(const uint16_t* __restrict__ q, int T, int Hq,
+                                                    int Hkv, int D,
+                                                    const float* __restrict__ means,
+                                                    const int* __restrict__ cu_chunk, int nchunk,
+                                                    const int* __restrict__ chunk_batch,
+                                                    const int* __restrict__ first_chunk, int R,
+                                                    int F, int* __restrict__ sel,
+                                                    float* __restrict__ gate) {
+  const int s = blockIdx.x * 256 + threadIdx.x;
+  const int h = blockIdx.y;
+  if (s >= T) return;
   const int G = Hq / Hkv, kh = h / G;
   // chunk containing s
   int lo = 0, hi = nchunk - 1;
@@ -73,7 +101,11 @@ __global__ void route_kernel(const uint16_t* __restrict__ q, int T, int Hq, int 
     if (cu_chunk[mid] <= s) lo = mid; else hi = mid - 1;
   }
   const int cs = lo, b = chunk_batch[cs], c0 = first_chunk[cs];
-  const uint16_t* qr = q + idx * D;
+  const int64_t idx = (int64_t)s * Hq + h;
+  constexpr int NQ = DP / 8;
+  u16x8_t qv[NQ];
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) qv[i] = i * 8 < D ? ld8(q + idx * D + i * 8) : zero8();
 
   float val[kMaxRemote];
   int ix[kMaxRemote];
@@ -83,19 +115,21 @@ __global__ void route_kernel(const uint16_t* __restrict__ q, int T, int Hq, int 
 
   for (int c = c0; c < cs; ++c) {
     const float* mr = means + ((int64_t)(c - b) * Hkv + kh) * D;
+    // sequential fma chain over d = 0 .. D-1
     float acc = 0.0f;
-    for (int d = 0; d < D; d += 8) {
-      u16x8_t qv = ld8(qr + d);
-      f32x4_t m0 = *reinterpret_cast<const f32x4_t*>(mr + d);
-      f32x4_t m1 = *reinterpret_cast<const f32x4_t*>(mr + d + 4);
-      acc = fmaf(m0[0], to_f32<DT>(qv[0]), acc);
-      acc = fmaf(m0[1], to_f32<DT>(qv[1]), acc);
-      acc = fmaf(m0[2], to_f32<DT>(qv[2]), acc);
-      acc = fmaf(m0[3], to_f32<DT>(qv[3]), acc);
-      acc = fmaf(m1[0], to_f32<DT>(qv[4]), acc);
-      acc = fmaf(m1[1], to_f32<DT>(qv[5]), acc);
-      acc = fmaf(m1[2], to_f32<DT>(qv[6]), acc);
-      acc = fmaf(m1[3], to_f32<DT>(qv[7]), acc);
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      if (i * 8 >= D) break;
+      const f32x4_t m0 = *reinterpret_cast<const f32x4_t*>(mr + i * 8);
+      const f32x4_t m1 = *reinterpret_cast<const f32x4_t*>(mr + i * 8 + 4);
+      acc = fmaf(m0[0], to_f32<DT>(qv[i][0]), acc);
+      acc = fmaf(m0[1], to_f32<DT>(qv[i][1]), acc);
+      acc = fmaf(m0[2], to_f32<DT>(qv[i][2]), acc);
+      acc = fmaf(m0[3], to_f32<DT>(qv[i][3]), acc);
+      acc = fmaf(m1[0], to_f32<DT>(qv[i][4]), acc);
+      acc = fmaf(m1[1], to_f32<DT>(qv[i][5]), acc);
+      acc = fmaf(m1[2], to_f32<DT>(qv[i][6]), acc);
+      acc = fmaf(m1[3], to_f32<DT>(qv[i][7]), acc);
     }
     if (gate) gate[((int64_t)(c - b) * Hq + h) * T + s] = acc;
     // stable insertion into the descending list: equal scores stay behind the
@@ -156,15 +190,22 @@ MOBA_DEV ExpertRange expert_range(int e, int Hq, int Hkv, const int* cu_chunk,
   return r;
 }
 
+// Candidates of an expert are split in blocks of kCandBlock; workgroup
+// (e, b) handles block b of expert e.  Block counts go to work[e * nbmax + b]
+// and become exclusive offsets within the expert in the scan, so the fill is
+// an ordered compaction with no atomics.
+constexpr int kCandBlock = 2048;
+
 __global__ __launch_bounds__(256) void expert_count_kernel(
     const int* __restrict__ sel, int Hq, int Hkv, int R, const int* __restrict__ cu_chunk,
     const int* __restrict__ chunk_batch, const int* __restrict__ cu_seqlens,
-    const int* __restrict__ filtered, int* __restrict__ counts) {
-  const int e = blockIdx.x;
+    const int* __restrict__ filtered, int nbmax, int* __restrict__ work) {
+  const int e = blockIdx.x, b = blockIdx.y;
   ExpertRange x = expert_range(e, Hq, Hkv, cu_chunk, chunk_batch, cu_seqlens, filtered);
   const int64_t n = (int64_t)x.G * x.ns;
+  const int64_t i1 = min(n, (int64_t)(b + 1) * kCandBlock);
   int cnt = 0;
-  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+  for (int64_t i = (int64_t)b * kCandBlock + threadIdx.x; i < i1; i += 256) {
     const int g = (int)(i / x.ns), s = x.s0 + (int)(i % x.ns);
     cnt += find_slot(sel, (int64_t)s * Hq + x.kh * x.G + g, R, x.c) >= 0;
   }
@@ -174,12 +215,14 @@ __global__ __launch_bounds__(256) void expert_count_kernel(
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   if (lane == 0) part[w] = cnt;
   __syncthreads();
-  if (threadIdx.x == 0) counts[e] = part[0] + part[1] + part[2] + part[3];
+  if (threadIdx.x == 0) work[(int64_t)e * nbmax + b] = part[0] + part[1] + part[2] + part[3];
 }
 
-// Exclusive scans of row counts and tile counts (one workgroup).
-__global__ __launch_bounds__(1024) void expert_scan_kernel(const int* __restrict__ counts, int E,
-                                                         int block_rows, int* __restrict__ row_off,
+// Per expert: block counts -> exclusive block offsets and the row count; then
+// exclusive scans of row counts and tile counts over the experts (one workgroup).
+__global__ __launch_bounds__(1024) void expert_scan_kernel(int* __restrict__ work, int nbmax, int E,
+                                                         int block_rows, int* __restrict__ counts,
+                                                         int* __restrict__ row_off,
                                                          int* __restrict__ tile_off) {
   __shared__ int wr[16], wt[16];
   __shared__ int carry_r, carry_t;
@@ -188,7 +231,12 @@ __global__ __launch_bounds__(1024) void expert_scan_kernel(const int* __restrict
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   for (int base = 0; base < E; base += 1024) {
     const int e = base + threadIdx.x;
-    int r = e < E ? counts[e] : 0;
+    int r = 0;
+    if (e < E) {
+      int* wb = work + (int64_t)e * nbmax;
+      for (int b = 0; b < nbmax; ++b) { const int c = wb[b]; wb[b] = r; r += c; }
+      counts[e] = r;
+    }
     int t = (r + block_rows - 1) / block_rows;
     // inclusive wave scan
     int ir = r, it = t;
@@ -213,17 +261,20 @@ __global__ __launch_bounds__(1024) void expert_scan_kernel(const int* __restrict
 __global__ __launch_bounds__(256) void expert_fill_kernel(
     const int* __restrict__ sel, int Hq, int Hkv, int R, const int* __restrict__ cu_chunk,
     const int* __restrict__ chunk_batch, const int* __restrict__ cu_seqlens,
-    const int* __restrict__ filtered, const int* __restrict__ row_off, int* __restrict__ rows) {
-  const int e = blockIdx.x;
+    const int* __restrict__ filtered, const int* __restrict__ row_off, int nbmax,
+    const int* __restrict__ work, int* __restrict__ rows) {
+  const int e = blockIdx.x, b = blockIdx.y;
   ExpertRange x = expert_range(e, Hq, Hkv, cu_chunk, chunk_batch, cu_seqlens, filtered);
   const int64_t n = (int64_t)x.G * x.ns;
+  const int64_t i0 = (int64_t)b * kCandBlock, i1 = min(n, i0 + kCandBlock);
+  if (i0 >= i1) return;
   __shared__ int wtot[4];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  int out = row_off[e];
-  for (int64_t base = 0; base < n; base += 256) {
+  int out = row_off[e] + work[(int64_t)e * nbmax + b];
+  for (int64_t base = i0; base < i1; base += 256) {
     const int64_t i = base + threadIdx.x;
     int slot = -1, h = 0, s = 0;
-    if (i < n) {
+    if (i < i1) {
       const int g = (int)(i / x.ns);
       s = x.s0 + (int)(i % x.ns);
       h = x.kh * x.G + g;
@@ -242,6 +293,10 @@ __global__ __launch_bounds__(256) void expert_fill_kernel(
   }
 }
 
+int64_t expert_blocks(int T, int Hq, int Hkv) {
+  return ((int64_t)(Hq / Hkv) * T + kCandBlock - 1) / kCandBlock;
+}
+
 }  // namespace
 
 extern "C" int moba_hip_chunk_means(const void* k, int dtype, int T, int Hkv, int D,
@@ -251,14 +306,23 @@ extern "C" int moba_hip_chunk_means(const void* k, int dtype, int T, int Hkv, in
   if (F <= 0) return MOBA_OK;
   if (dtype != 0 && dtype != 1) { moba_set_error("chunk_means: dtype must be 0 (bf16) or 1 (fp16)"); return MOBA_ERR_ARG; }
   if (D < 8 || D % 8 || Hkv < 1 || chunk < 1) { moba_set_error("chunk_means: bad shape"); return MOBA_ERR_ARG; }
-  dim3 grid((unsigned)((int64_t)F * Hkv * (D / 8))), block(64);
+  if (D > 256) { moba_set_error("chunk_means: head_dim must be at most 256"); return MOBA_ERR_ARG; }
+  dim3 grid((unsigned)((int64_t)F * Hkv)), block(256);
+  const size_t lds = (size_t)64 * D * sizeof(float);
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == 0)
-    hipLaunchKernelGGL(chunk_means_kernel<0>, grid, block, 0, st, (const uint16_t*)k, Hkv, D,
-                       chunk_start, chunk, precision, means);
-  else
-    hipLaunchKernelGGL(chunk_means_kernel<1>, grid, block, 0, st, (const uint16_t*)k, Hkv, D,
-                       chunk_start, chunk, precision, means);
+  const uint16_t* kp = (const uint16_t*)k;
+#define MOBA_MEANS(DT_, NP_) \
+  hipLaunchKernelGGL((chunk_means_kernel<DT_, NP_>), grid, block, lds, st, kp, Hkv, D, chunk_start, \
+                     chunk, precision, means)
+  const int nd8 = D / 8;
+  if (dtype == 0) {
+    if (nd8 <= 4) MOBA_MEANS(0, 1); else if (nd8 <= 8) MOBA_MEANS(0, 2);
+    else if (nd8 <= 16) MOBA_MEANS(0, 4); else MOBA_MEANS(0, 8);
+  } else {
+    if (nd8 <= 4) MOBA_MEANS(1, 1); else if (nd8 <= 8) MOBA_MEANS(1, 2);
+    else if (nd8 <= 16) MOBA_MEANS(1, 4); else MOBA_MEANS(1, 8);
+  }
+#undef MOBA_MEANS
   return moba_launch_status("chunk_means");
 }
 
@@ -275,33 +339,45 @@ extern "C" int moba_hip_route_prefill(const void* q, int dtype, int T, int Hq, i
     hipLaunchKernelGGL(fill_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, gate,
                        n, -INFINITY);
   }
-  const int64_t n = (int64_t)T * Hq;
-  dim3 grid((unsigned)((n + 255) / 256)), block(256);
-  if (dtype == 0)
-    hipLaunchKernelGGL(route_kernel<0>, grid, block, 0, st, (const uint16_t*)q, T, Hq, Hkv, D,
-                       means, cu_chunk, nchunk, chunk_batch, first_chunk, R, F, sel, gate);
-  else
-    hipLaunchKernelGGL(route_kernel<1>, grid, block, 0, st, (const uint16_t*)q, T, Hq, Hkv, D,
-                       means, cu_chunk, nchunk, chunk_batch, first_chunk, R, F, sel, gate);
+  if (D > 256) { moba_set_error("route_prefill: head_dim must be at most 256"); return MOBA_ERR_ARG; }
+  dim3 grid((unsigned)((T + 255) / 256), (unsigned)Hq), block(256);
+  const uint16_t* qp = (const uint16_t*)q;
+#define MOBA_ROUTE(DT_, DP_) \
+  hipLaunchKernelGGL((route_kernel<DT_, DP_>), grid, block, 0, st, qp, T, Hq, Hkv, D, means, \
+                     cu_chunk, nchunk, chunk_batch, first_chunk, R, F, sel, gate)
+  if (dtype == 0) {
+    if (D <= 64) MOBA_ROUTE(0, 64); else if (D <= 128) MOBA_ROUTE(0, 128); else MOBA_ROUTE(0, 256);
+  } else {
+    if (D <= 64) MOBA_ROUTE(1, 64); else if (D <= 128) MOBA_ROUTE(1, 128); else MOBA_ROUTE(1, 256);
+  }
+#undef MOBA_ROUTE
   return moba_launch_status("route_prefill");
+}
+
+extern "C" int64_t moba_hip_pack_experts_work(int T, int Hq, int Hkv, int F) {
+  if (T < 0 || Hq < 1 || Hkv < 1 || Hq % Hkv || F < 0) return -1;
+  return (int64_t)F * Hkv * expert_blocks(T, Hq, Hkv);
 }
 
 extern "C" int moba_hip_pack_experts(const int* sel, int T, int Hq, int Hkv, int R,
                                      const int* cu_chunk, const int* chunk_batch,
                                      const int* cu_seqlens, const int* filtered, int F,
                                      int block_rows, int* counts, int* row_off, int* tile_off,
-                                     int* rows, void* stream) {
-  (void)T;
+                                     int* rows, int* work, void* stream) {
   if (F <= 0) return MOBA_OK;
   if ((int64_t)T * Hq * R >= (1ll << 31) || (int64_t)T * Hq >= (1ll << 28)) { moba_set_error("pack_experts: T*Hq*R exceeds int32 or T*Hq exceeds 2^28"); return MOBA_ERR_ARG; }
   if (R > 8) { moba_set_error("pack_experts: at most 8 remote chunks per query"); return MOBA_ERR_ARG; }
+  if (Hkv < 1 || Hq % Hkv) { moba_set_error("pack_experts: Hq must be a multiple of Hkv"); return MOBA_ERR_ARG; }
+  if (work == nullptr) { moba_set_error("pack_experts: the work buffer (moba_hip_pack_experts_work ints) is required"); return MOBA_ERR_ARG; }
   hipStream_t st = (hipStream_t)stream;
   const int E = F * Hkv;
-  hipLaunchKernelGGL(expert_count_kernel, dim3(E), dim3(256), 0, st, sel, Hq, Hkv, R, cu_chunk,
-                     chunk_batch, cu_seqlens, filtered, counts);
-  hipLaunchKernelGGL(expert_scan_kernel, dim3(1), dim3(1024), 0, st, counts, E, block_rows,
-                     row_off, tile_off);
-  hipLaunchKernelGGL(expert_fill_kernel, dim3(E), dim3(256), 0, st, sel, Hq, Hkv, R, cu_chunk,
-                     chunk_batch, cu_seqlens, filtered, row_off, rows);
+  const int nbmax = (int)expert_blocks(T, Hq, Hkv);
+  if (nbmax < 1) return MOBA_OK;
+  hipLaunchKernelGGL(expert_count_kernel, dim3(E, nbmax), dim3(256), 0, st, sel, Hq, Hkv, R,
+                     cu_chunk, chunk_batch, cu_seqlens, filtered, nbmax, work);
+  hipLaunchKernelGGL(expert_scan_kernel, dim3(1), dim3(1024), 0, st, work, nbmax, E, block_rows,
+                     counts, row_off, tile_off);
+  hipLaunchKernelGGL(expert_fill_kernel, dim3(E, nbmax), dim3(256), 0, st, sel, Hq, Hkv, R,
+                     cu_chunk, chunk_batch, cu_seqlens, filtered, row_off, nbmax, work, rows);
   return moba_launch_status("pack_experts");
 }

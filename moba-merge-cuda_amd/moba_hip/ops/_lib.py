@@ -22,7 +22,8 @@ SIGNATURES = {
     "moba_hip_last_error": [],
     "moba_hip_chunk_means": [_P, _I, _I, _I, _I, _P, _I, _I, _I, _P, _P],
     "moba_hip_route_prefill": [_P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _I, _I, _P, _P, _P],
-    "moba_hip_pack_experts": [_P, _I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _P, _P, _P, _P, _P],
+    "moba_hip_pack_experts": [_P, _I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _P, _P, _P, _P, _P, _P],
+    "moba_hip_pack_experts_work": [_I, _I, _I, _I],
     "moba_hip_prefill_fwd": [_P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _I, _P, _I, _P, _I,
                              _P, _P, _P, _P, _I, _P, _P, _P, _P, _P],
     "moba_hip_prefill_bwd": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _I, _P, _I,
@@ -42,7 +43,7 @@ SIGNATURES = {
     "moba_hip_decode_fused": [_P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _I, _P, _P, _P, _P,
                               _P, _I, _I, _I, _I, _I, _I, _I, _P, _I, _P, _P, _P, _P, _P, _P],
 }
-_RESTYPES = {"moba_hip_last_error": ctypes.c_char_p}
+_RESTYPES = {"moba_hip_last_error": ctypes.c_char_p, "moba_hip_pack_experts_work": ctypes.c_int64}
 
 _lib = None
 _lock = threading.Lock()

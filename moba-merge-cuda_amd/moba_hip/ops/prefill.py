@@ -174,6 +174,8 @@ def route(plan: PrefillPlan, q, k, precision: int, want_gate=False):
     r.tile_off = torch.empty(E + 1, dtype=torch.int32, device=dev)
     r.rows = torch.empty(max(1, T * hq * R), dtype=torch.int32, device=dev)
     gate = torch.empty((F, hq, T), dtype=torch.float32, device=dev) if want_gate else None
+    work = torch.empty(max(1, _lib.load().moba_hip_pack_experts_work(T, hq, plan.hkv, F)),
+                       dtype=torch.int32, device=dev)
     _lib.call("moba_hip_chunk_means", k.data_ptr(), code, T, plan.hkv, d,
               plan.ptr("chunk_start"), F, plan.chunk, precision, r.means.data_ptr(), st)
     _lib.call("moba_hip_route_prefill", q.data_ptr(), code, T, hq, plan.hkv, d,
@@ -183,7 +185,7 @@ def route(plan: PrefillPlan, q, k, precision: int, want_gate=False):
     _lib.call("moba_hip_pack_experts", r.sel.data_ptr(), T, hq, plan.hkv, R,
               plan.ptr("cu_chunk"), plan.ptr("chunk_batch"), plan.ptr("cu_seqlens"),
               plan.ptr("filtered"), F, plan.block_rows, r.counts.data_ptr(), r.row_off.data_ptr(),
-              r.tile_off.data_ptr(), r.rows.data_ptr(), st)
+              r.tile_off.data_ptr(), r.rows.data_ptr(), work.data_ptr(), st)
     return (r, gate) if want_gate else r
 
 

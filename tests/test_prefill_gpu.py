@@ -43,6 +43,9 @@ def _gpu_route(q, k, cu, cfg, precision=0):
     (8, 1, 128, (129, 257), 32, 3),
     (14, 2, 64, (600,), 64, 3),
     (6, 3, 40, (17, 1, 90), 8, 9),
+    # many candidate blocks of 2048 per expert (multi-workgroup compaction)
+    (14, 2, 64, (12000, 3000), 512, 4),
+    (8, 8, 128, (4100,), 512, 3),
 ])
 def test_routing_bit_exact(cuda_device, hq, hkv, dim, lens, chunk, topk, dtype, precision):
     q, k, v, cu, ml, _ = prefill_inputs(hq, hkv, dim, lens, dtype, seed=7)
@@ -57,13 +60,25 @@ def test_routing_bit_exact(cuda_device, hq, hkv, dim, lens, chunk, topk, dtype, 
     fin = np.isfinite(gate_ref)
     np.testing.assert_array_equal(g[fin].view(np.uint32), gate_ref[fin].view(np.uint32))
     np.testing.assert_array_equal(rt.sel.cpu().numpy(), sel)
-    # expert lists: every selected (s,h,j) appears exactly once, grouped by expert
+    # expert lists in the reference's order: expert e = f*Hkv + kv head, and
+    # within it (group head g, token s) g-major, as the nonzero over
+    # [F*Hkv, G*T] in grouped_attention.py:78-86 enumerates them
     counts = rt.counts.cpu().numpy()
+    row_off = rt.row_off.cpu().numpy()
     rows = rt.rows.cpu().numpy()[: counts.sum()]
-    R = remote
-    expect = sorted((((s * hq + h) << 3) | j) for s in range(q.shape[0]) for h in range(hq)
-                    for j in range(R) if sel[s, h, j] >= 0)
-    assert sorted(rows.tolist()) == expect
+    R, G = remote, hq // hkv
+    cu_l = cu.tolist()
+    for f, c in enumerate(filtered):
+        b = next(i for i in range(len(cu_l) - 1) if cu_l[i] <= cu_chunk[c] < cu_l[i + 1])
+        for kh in range(hkv):
+            e = f * hkv + kh
+            expect = [(((s * hq + kh * G + g) << 3) | j)
+                      for g in range(G) for s in range(cu_chunk[c + 1], cu_l[b + 1])
+                      for j in range(R) if sel[s, kh * G + g, j] == c]
+            assert counts[e] == len(expect)
+            got = rows[row_off[e]: row_off[e] + counts[e]].tolist()
+            assert got == expect, f"expert {e}"
+    assert row_off[-1] == len(rows)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
