@@ -78,12 +78,19 @@ int moba_hip_pack_experts(const int* sel, int T, int Hq, int Hkv, int R,
  * bad shape).  Helper of the entry above; no counterpart in the reference. */
 int64_t moba_hip_pack_experts_work(int T, int Hq, int Hkv, int F);
 
+/* Query rows per prefill tile for head dim D (-1 for an unsupported D): the
+ * block_rows of moba_hip_pack_experts and the row step of the self tiles
+ * passed to moba_hip_prefill_fwd / _bwd.  Helper of those entries; no
+ * counterpart in the reference. */
+int moba_hip_prefill_rows(int D);
+
 /* Sparse block attention forward + global-softmax merge.
  * Replaces OptMixedAttention.forward (src/moba_opt/mixed_attention.py:42-139):
  * both _flash_attn_varlen_forward calls and merge_forward_cuda
  * (src/moba_opt/ops/merge.cu:187-288).
  * q [T,Hq,D], k/v [T,Hkv,D]; self_tiles[n_self_tiles][2] = (chunk, first row)
- * tiles of 256 rows (128 when D > 128); sel/R, filtered[F] and the pack_experts outputs describe
+ * tiles of moba_hip_prefill_rows(D) rows; sel/R, filtered[F] and the pack_experts outputs (with
+ * block_rows = moba_hip_prefill_rows(D)) describe
  * the remote rows (R = 0: self branch only, e.g. the full-causal fallback with
  * one chunk per sequence).  max_remote_tiles bounds tile_off[E].
  * part_o [T*Hq*R, D] fp32 and part_ml [T*Hq*R, 2] fp32 (per-slot softmax

@@ -7,13 +7,13 @@
 // src/moba_opt/ops/merge.cu:27-153.
 //
 // Two launches, no atomics, no packed copies of Q or K/V:
-//  * remote_kernel: one workgroup per tile of <=256 rows of one expert
+//  * remote launch: one workgroup per tile of 128 rows of one expert
 //    (filtered chunk, kv head).  Rows are read in place from q[T,Hq,D] through
 //    the expert's row list; the chunk's K/V tiles are staged in LDS once per
 //    workgroup.  Each row writes a normalised partial o and its (max, sum)
 //    softmax statistics into its slot
 //    (s*Hq + h)*R + j, j = rank of the chunk in the row's ascending selection.
-//  * self_kernel: one workgroup per (chunk, q head, 256 consecutive rows),
+//  * self launch: one workgroup per (chunk, q head, 128 consecutive rows),
 //    causal within the chunk; its epilogue merges the row's partials in
 //    ascending-slot order (global softmax: m = max l, O = sum e^{l-m} o / z,
 //    L = m + log z) and writes the final O (input dtype) and LSE (fp32).
@@ -390,6 +390,14 @@ int dispatch_fwd(const FwdArgs& a, int n_self, int max_remote, hipStream_t st) {
 }
 
 }  // namespace
+
+extern "C" int moba_hip_prefill_rows(int D) {
+  if (D < 8 || D > 256 || D % 8) return -1;
+  if (D <= 32) return 128 * attn_qb<32>();
+  if (D <= 64) return 128 * attn_qb<64>();
+  if (D <= 128) return 128 * attn_qb<128>();
+  return 128 * attn_qb<256>();
+}
 
 extern "C" int moba_hip_prefill_fwd(const void* q, const void* k, const void* v, int dtype, int T,
                                     int Hq, int Hkv, int D, float scale, const int* cu_chunk,

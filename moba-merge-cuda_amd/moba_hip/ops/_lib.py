@@ -24,6 +24,7 @@ SIGNATURES = {
     "moba_hip_route_prefill": [_P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _I, _I, _P, _P, _P],
     "moba_hip_pack_experts": [_P, _I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _P, _P, _P, _P, _P, _P],
     "moba_hip_pack_experts_work": [_I, _I, _I, _I],
+    "moba_hip_prefill_rows": [_I],
     "moba_hip_prefill_fwd": [_P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _I, _P, _I, _P, _I,
                              _P, _P, _P, _P, _I, _P, _P, _P, _P, _P],
     "moba_hip_prefill_bwd": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _I, _P, _I,

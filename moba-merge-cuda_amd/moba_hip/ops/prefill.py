@@ -18,8 +18,12 @@ DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1}
 
 
 def attn_rows(head_dim):
-    """Query rows per forward / dQ workgroup: 4 waves x 32 rows."""
-    return 128
+    """Query rows per prefill tile (self tiles and expert tiles), as the
+    library's kernels expect them for this head dim."""
+    rows = _lib.load().moba_hip_prefill_rows(head_dim)
+    if rows <= 0:
+        raise ValueError(f"unsupported head_dim {head_dim}")
+    return rows
 
 
 def dkdv_keys(head_dim):
