@@ -308,6 +308,7 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
                     uint16_t* Qn, uint16_t* Gn, float* Ln) __attribute__((always_inline)) {
       const Cur tn = cur_next(tc);
       dma(Qn, Gn, Ln, tn);
+      __builtin_amdgcn_sched_barrier(0);  // the next tile's loads go out first
       const bool cur = tc.it < it_hi && !skipped(tc);
       if constexpr (ROLE_P) p_step(Qc, Lc, Gp, tc, cur, pv);
       else d_step(Gc, Qp, Lp, tc, cur, pv);

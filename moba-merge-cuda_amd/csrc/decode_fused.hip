@@ -290,10 +290,13 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
         float u[32];
 #pragma unroll
         for (int i = 0; i < 32; ++i) u[i] = sg[c0 + i];
+        // one comparison at a time: hoisted together, their lane masks
+        // exhausted the scalar registers and spilled
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
           const int ci = c0 + i;
           rank += (int)((ci < legal) & ((u[i] > v) | ((u[i] == v) & (ci < c))));
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
       if (rank < a.R) {

@@ -165,3 +165,26 @@ def test_graph_replays_match_eager(cuda_device):
             torch.cuda.synchronize()
             assert torch.equal(a.output, b.output) and torch.equal(a.lse, b.lse)
             assert torch.equal(a.selected_blocks, b.selected_blocks)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_prepared_route_ties_pick_lowest_chunks(cuda_device, dtype):
+    """Constant keys make every closed chunk's gate score equal: the fused
+    route must then pick the lowest chunks, in order, exactly as the oracle's
+    (score desc, chunk asc) rule does (kv_cache.py:208-223 top-k semantics)."""
+    cache = _paged()(2, 60, 2, 64, page_size=5, chunk_size=4, dtype=dtype)
+    k = torch.ones((30, 2, 64), dtype=dtype, device="cuda")
+    v = rand((30, 2, 64), dtype, 601)
+    cache.append(k, v, sequence_ids=[1, 0], cu_seqlens=[0, 13, 30])
+    with cache.prepare_decode([1, 0], 12, topk=4) as plan:
+        for step in range(6):
+            q = rand((2, 12, 64), dtype, 610 + step)
+            kn = torch.ones((2, 2, 64), dtype=dtype, device="cuda")
+            vn = rand((2, 2, 64), dtype, 630 + step)
+            result = plan.step(q, kn, vn)
+            check(cache, result, q)
+            sel = result.selected_blocks.cpu()
+            for row in range(2):
+                cur = int(sel[row, 0, 0])
+                want = list(range(min(3, cur)))
+                assert sel[row, :, 1:1 + len(want)].tolist() == [want] * 12
