@@ -283,22 +283,31 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
       const float* sg = sc + g * width;
       const float v = sg[c];
       if (!(v > -INFINITY)) continue;
-      int rank = 0;
-      // 32 scores per batch, all read before the comparisons; no branches
-      // (reads past `legal` stay inside the route scratch and are masked)
+      // 32 scores per batch, all read before the comparisons, entries past
+      // `legal` as -inf (the reads stay inside the route scratch).  Count the
+      // higher scores and the equal ones (v itself included); only exact ties
+      // need the chunk order, in a per-lane pass over the lower chunks.
+      int gt = 0, eq = 0;
       for (int c0 = 0; c0 < legal; c0 += 32) {
         float u[32];
 #pragma unroll
         for (int i = 0; i < 32; ++i) u[i] = sg[c0 + i];
+        if (c0 + 32 > legal) {
+#pragma unroll
+          for (int i = 0; i < 32; ++i) u[i] = c0 + i < legal ? u[i] : -INFINITY;
+        }
         // one comparison at a time: hoisted together, their lane masks
         // exhausted the scalar registers and spilled
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
-          const int ci = c0 + i;
-          rank += (int)((ci < legal) & ((u[i] > v) | ((u[i] == v) & (ci < c))));
+          gt += (int)(u[i] > v);
+          eq += (int)(u[i] == v);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
+      int rank = gt;
+      if (eq > 1)
+        for (int j = 0; j < c; ++j) rank += (int)(sg[j] == v);
       if (rank < a.R) {
         sel_s[g * S1 + 1 + rank] = c;
         atomicOr(&umask[c], 1 << g);

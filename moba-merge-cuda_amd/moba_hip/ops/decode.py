@@ -203,6 +203,26 @@ def launch_fused(args, stream):
     _lib.call("moba_hip_decode_fused", *args, stream)
 
 
+class FusedLauncher:
+    """``moba_hip_decode_fused`` with its arguments converted to ctypes values
+    once (every pointer is a persistent workspace), so a launch converts only
+    the stream."""
+    __slots__ = ("fn", "args", "err")
+
+    def __init__(self, args):
+        lib = _lib.load()
+        self.fn = lib.moba_hip_decode_fused
+        self.err = lib.moba_hip_last_error
+        types = self.fn.argtypes[:-1]
+        self.args = tuple(None if a is None else t(a) for t, a in zip(types, args))
+
+    def __call__(self, stream):
+        rc = self.fn(*self.args, stream)
+        if rc != 0:
+            msg = self.err().decode(errors="replace")
+            raise _lib.MobaHipError(f"moba_hip_decode_fused failed ({rc}): {msg}")
+
+
 def fused(q, k, v, kc, vc, table, lengths, ids, positions, delta, means, chunk, width, remote,
           dense, pos_mode, selected, work: FusedWork, out, lse):
     """One-launch decode (route + attention; step mode also appends)."""

@@ -5,9 +5,10 @@ arguments, ``step`` / ``attend`` / ``capture`` / ``close``, context-manager use,
 lifecycle errors and the aliasing rule that outputs are persistent workspaces
 overwritten by the next call).
 
-One step is ONE launch of decode_fused (page-table delta, positions, route,
-stable top-k, paged attention, scatter of the new token, closing-chunk mean,
-length advance) when the shape allows (Hq/Hkv <= 16, head_dim a multiple of
+One step is ONE call of decode_fused: a fused kernel (page-table delta,
+positions, route, stable top-k, paged attention into split partials, scatter
+of the new token, closing-chunk mean) and the split merge (output, LSE,
+length advance), when the shape allows (Hq/Hkv <= 16, head_dim a multiple of
 8); otherwise the fixed sequence
     decode_step (page-table delta + positions + scatter + closing-chunk mean)
     -> decode_route (scores + stable top-k + slot list + work list)
@@ -22,6 +23,8 @@ rule (descending score, ties -> lowest chunk), so ``stable_routes`` only
 documents the behaviour.
 """
 from __future__ import annotations
+
+import contextlib
 
 import torch
 
@@ -45,6 +48,9 @@ class PreparedDecode:
             self.stable_routes = stable_routes
             self.dense = _mode(mode, topk)
             self.cache = cache
+            self._dev_index = torch.device(cache.device).index
+            if self._dev_index is None:
+                self._dev_index = torch.cuda.current_device()
             self._state = IncrementalLayout(cache._layout, _ints(sequence_ids, "sequence_ids"))
             self.ids = self._state.ids
             b, h, d = len(self.ids), self.num_q_heads, cache.head_dim
@@ -101,14 +107,23 @@ class PreparedDecode:
             return tuple(map(tuple, self._state.tables))
 
     def _check(self):
+        """Lifecycle and stream checks; returns the (current) cache stream."""
         if self.closed or self.cache._prepared_owner is not self:
             raise ValueError("prepared decode is closed or no longer owns cache")
         if self.failed:
             raise RuntimeError("CUDA execution failed; discard prepared decode and cache")
         if torch.cuda.is_current_stream_capturing():
             raise ValueError("use capture(), not external capture")
-        if torch.cuda.current_stream(self.cache.device).cuda_stream != self.cache._stream:
+        stream = torch.cuda.current_stream(self.cache.device).cuda_stream
+        if stream != self.cache._stream:
             raise ValueError("cross-stream cache access is unsupported")
+        return stream
+
+    def _device(self):
+        """The cache's device as the current device (no switch when it is)."""
+        if torch.cuda.current_device() == self._dev_index:
+            return contextlib.nullcontext()
+        return torch.cuda.device(self.cache.device)
 
     def _input(self, tensor, target, name):
         if tensor is target:  # the persistent workspace itself: shape/dtype/storage hold
@@ -158,21 +173,22 @@ class PreparedDecode:
             self._fused.set_schedule(entries, splits)
         self._sched_pos = list(positions)
 
-    def _compute(self, append):
+    def _compute(self, append, stream=None):
         c = self.cache
         if self._fused is not None:
             if self._fused_args is None:  # every pointer is a persistent workspace
                 self._fused_args = {
-                    mode: kernels.fused_args(
+                    mode: kernels.FusedLauncher(kernels.fused_args(
                         self.q, self.k if mode == 2 else None, self.v if mode == 2 else None,
                         c.k_cache, c.v_cache, c._table, c._lengths, self.gpu_ids,
                         self.positions, self.delta, c._means, c.chunk_size,
                         self.scores.shape[-1], self.remote, self.dense, mode,
                         None if self.dense else self.selected, self._fused, self.output,
-                        self.lse)
+                        self.lse))
                     for mode in (1, 2)}
-            kernels.launch_fused(self._fused_args[2 if append else 1],
-                                 torch.cuda.current_stream(c.device).cuda_stream)
+            if stream is None:
+                stream = torch.cuda.current_stream(c.device).cuda_stream
+            self._fused_args[2 if append else 1](stream)
             return
         if append:  # metadata + scatter + closing-chunk mean in one launch
             kernels.step(c._table, c._lengths, self.gpu_ids, self.positions, self.delta, self.k,
@@ -187,12 +203,12 @@ class PreparedDecode:
                           self.positions, self._work, self.output, self.lse, c.chunk_size,
                           self.dense, self.max_chunks, self._part_o, self._part_ml)
 
-    def _run(self, kind, use_graph):
+    def _run(self, kind, use_graph, stream):
         try:
             if use_graph:
                 self._graphs[kind].replay()
             else:
-                self._compute(kind == "step")
+                self._compute(kind == "step", stream)
         except Exception:
             self.failed = True
             raise
@@ -201,10 +217,11 @@ class PreparedDecode:
         return DecodeResult(self.output, self.lse, None if self.dense else self.selected,
                             self.ids, positions)
 
-    @torch.no_grad()
     def attend(self, q, *, use_graph=False):
-        with self.cache._lock, torch.cuda.device(self.cache.device):
-            self._check()
+        # no autograd: inputs that require grad are rejected and every op
+        # here is an in-place copy or a library launch
+        with self.cache._lock, self._device():
+            stream = self._check()
             self._input(q, self.q, "q")
             pos = tuple(self._state.lengths[s] - 1 for s in self.ids)
             if min(pos) < 0:
@@ -214,14 +231,13 @@ class PreparedDecode:
             if q is not self.q:
                 self.q.copy_(q)
             self._schedule(pos)
-            self._run("attend", use_graph)
+            self._run("attend", use_graph, stream)
             return self._result(pos)
 
-    @torch.no_grad()
     def step(self, q, k, v, *, use_graph=False):
         """One token per fixed active row; validation/capacity errors change nothing."""
-        with self.cache._lock, torch.cuda.device(self.cache.device):
-            self._check()
+        with self.cache._lock, self._device():
+            stream = self._check()
             for tensor, target, name in ((q, self.q, "q"), (k, self.k, "k"), (v, self.v, "v")):
                 self._input(tensor, target, name)
             if use_graph and "step" not in self._graphs:
@@ -232,7 +248,7 @@ class PreparedDecode:
                     target.copy_(tensor)
             self._upload(plan)
             self._schedule(plan.positions)
-            self._run("step", use_graph)
+            self._run("step", use_graph, stream)
             self._state.commit(plan)
             return self._result(plan.positions)
 
