@@ -571,6 +571,9 @@ __global__ __launch_bounds__(64 * kMergeWaves) void merge_kernel(FusedArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int rh = blockIdx.x, qrow = rh / a.Hq, h = rh % a.Hq;
   const int S = a.sched != nullptr ? a.sched[3 * a.n_sched + qrow * a.Hkv + h / a.G] : a.smax;
+  // the row's position decides only whether anything is written: its loads
+  // (ids -> lengths) run beside the partial loads below, which stay inside
+  // the row's own slots either way
   const int sid = a.ids[qrow];
   int p;
   if (a.pos_mode == 0) {
@@ -579,21 +582,33 @@ __global__ __launch_bounds__(64 * kMergeWaves) void merge_kernel(FusedArgs a) {
     const int len = a.lengths[sid];
     p = a.pos_mode == 2 ? len : len - 1;
   }
-  if (p < 0 || p / a.C > a.width) return;  // the attention launch skipped this row
   const int64_t e0 = (int64_t)rh * a.smax;
   const int d = lane * 4;
   const bool dok = d < a.D;
   float m[kMergePer], z[kMergePer];
   f32x4_t o[kMergePer];
+  // Every slot below smax is in the row's allocation: all loads are issued
+  // unconditionally, back to back, and slots past S (stale or uninitialised,
+  // possibly NaN) are dropped by a select afterwards.  Guarded loads compiled
+  // to one branch and one full wait per slot.
+  const int dl = dok ? d : 0;
 #pragma unroll
   for (int i = 0; i < kMergePer; ++i) {
     const int s = w + kMergeWaves * i;
-    const bool ok = s < S;
-    m[i] = ok ? a.part_ml[2 * (e0 + s)] : -INFINITY;
-    z[i] = ok ? a.part_ml[2 * (e0 + s) + 1] : 0.0f;
-    o[i] = (ok && dok) ? *reinterpret_cast<const f32x4_t*>(a.part_o + (e0 + s) * a.D + d)
-                       : (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + 2 * (e0 + s));
+    m[i] = ml.x;
+    z[i] = ml.y;
+    o[i] = *reinterpret_cast<const f32x4_t*>(a.part_o + (e0 + s) * a.D + dl);
   }
+#pragma unroll
+  for (int i = 0; i < kMergePer; ++i) {
+    const bool ok = w + kMergeWaves * i < S;
+    m[i] = ok ? m[i] : -INFINITY;
+    z[i] = ok ? z[i] : 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[i][e] = (ok && dok) ? o[i][e] : 0.0f;
+  }
+  if (p < 0 || p / a.C > a.width) return;  // the attention launch skipped this row
   __shared__ float wm[kMergeWaves], wz[kMergeWaves];
   __shared__ f32x4_t wo[kMergeWaves][64];
   float mw = -INFINITY;
