@@ -358,19 +358,28 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[qb][db][r] *= a.scale;
+      // one slot per iteration, all of its loads issued together: slots
+      // below R are in the row's allocation, columns past D are clamped and
+      // masked, unselected slots (sel < 0) add zero
       for (int jj = 0; jj < a.R; ++jj) {
-        if (a.sel[row * a.R + jj] < 0) continue;
-        const float* po = a.part_dq + (row * a.R + jj) * D;
+        const int64_t sl = row * a.R + jj;
+        const bool on = a.sel[sl] >= 0;
+        const float* po = a.part_dq + sl * D;
+        f32x4_t o[NDB][4];
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int d0 = db * 32 + 8 * j + 4 * hh;
-            if (d0 < D) {
-              const f32x4_t o = *reinterpret_cast<const f32x4_t*>(po + d0);
+            o[db][j] = *reinterpret_cast<const f32x4_t*>(po + (d0 < D ? d0 : 0));
+          }
 #pragma unroll
-              for (int i = 0; i < 4; ++i) acc[qb][db][4 * j + i] += o[i];
-            }
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const bool ok = on && db * 32 + 8 * j + 4 * hh < D;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[qb][db][4 * j + i] += ok ? o[db][j][i] : 0.0f;
           }
       }
       uint16_t* orow = a.dq + row * D;

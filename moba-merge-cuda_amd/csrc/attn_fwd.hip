@@ -321,9 +321,16 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void fwd_kernel(FwdArgs 
       }
     } else {
       const int64_t row = (int64_t)s[qb] * a.Hq + h[qb];
+      // Slot loads are unconditional (slots below R are in the row's
+      // allocation) and masked after, so each pass costs one round trip per
+      // slot: guarded loads compiled to one full wait per load.
       float M2 = m_run[qb];
-      for (int jj = 0; jj < a.R; ++jj)
-        if (a.sel[row * a.R + jj] >= 0) M2 = fmaxf(M2, a.part_ml[2 * (row * a.R + jj)]);
+      for (int jj = 0; jj < a.R; ++jj) {
+        const int64_t sl = row * a.R + jj;
+        const int sv = a.sel[sl];
+        const float mv = a.part_ml[2 * sl];
+        M2 = sv >= 0 ? fmaxf(M2, mv) : M2;
+      }
       const float ws = fast_exp2(m_run[qb] - M2);
       float z = l * ws;
 #pragma unroll
@@ -331,21 +338,28 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void fwd_kernel(FwdArgs 
 #pragma unroll
         for (int r = 0; r < 16; ++r) oacc[qb][db][r] *= ws;
       for (int jj = 0; jj < a.R; ++jj) {
-        if (a.sel[row * a.R + jj] < 0) continue;
         const int64_t sl = row * a.R + jj;
-        const float w = a.part_ml[2 * sl + 1] * fast_exp2(a.part_ml[2 * sl] - M2);
-        z += w;
+        const int sv = a.sel[sl];
+        const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + 2 * sl);
         const float* po = a.part_o + sl * D;
+        f32x4_t o[NDB][4];
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int d0 = db * 32 + 8 * j + 4 * hh;
-            if (d0 < D) {
-              const f32x4_t o = *reinterpret_cast<const f32x4_t*>(po + d0);
+            o[db][j] = *reinterpret_cast<const f32x4_t*>(po + (d0 < D ? d0 : 0));
+          }
+        // an unselected slot's data may be stale or NaN: select, never 0 * x
+        const float w = sv >= 0 ? ml.y * fast_exp2(ml.x - M2) : 0.0f;
+        z += w;
 #pragma unroll
-              for (int i = 0; i < 4; ++i) oacc[qb][db][4 * j + i] += w * o[i];
-            }
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const bool ok = sv >= 0 && db * 32 + 8 * j + 4 * hh < D;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) oacc[qb][db][4 * j + i] += ok ? w * o[db][j][i] : 0.0f;
           }
       }
       const float invz = 1.0f / z;
