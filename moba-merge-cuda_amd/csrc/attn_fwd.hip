@@ -108,15 +108,18 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void fwd_kernel(FwdArgs 
       h[qb] = sh % a.Hq;
     }
   } else {
-    const int c = a.self_tiles[2 * blockIdx.x], row0 = a.self_tiles[2 * blockIdx.x + 1];
-    kh = blockIdx.y / a.G;
+    // grid (q head within the kv group, tile, kv head): the G heads that
+    // share a kv head's K/V run next to each other, then the next tile of the
+    // same kv head (tiles listed largest first)
+    const int c = a.self_tiles[2 * blockIdx.y], row0 = a.self_tiles[2 * blockIdx.y + 1];
+    kh = blockIdx.z;
     k_lo = a.cu_chunk[c];
     const int c_end = a.cu_chunk[c + 1];
     k_hi = min(c_end, k_lo + row0 + 128 * QB);
     s_wave0 = k_lo + row0 + wave * (32 * QB);
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-      h[qb] = blockIdx.y;
+      h[qb] = blockIdx.z * a.G + blockIdx.x;
       s[qb] = s_wave0 + qb * 32 + qi;
       valid[qb] = s[qb] < c_end;
       if (!valid[qb]) s[qb] = k_hi - 1;
@@ -389,7 +392,7 @@ int launch_fwd(const FwdArgs& a, int n_self_tiles, int max_remote_tiles, hipStre
     if (rc) return rc;
   }
   if (n_self_tiles > 0) {
-    hipLaunchKernelGGL((fwd_kernel<DT, DP, false, attn_qb<DP>()>), dim3(n_self_tiles, a.Hq), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((fwd_kernel<DT, DP, false, attn_qb<DP>()>), dim3(a.G, n_self_tiles, a.Hkv), dim3(256), 0, st, a);
     return moba_launch_status("prefill_fwd(self)");
   }
   return MOBA_OK;
@@ -424,7 +427,7 @@ extern "C" int moba_hip_prefill_fwd(const void* q, const void* k, const void* v,
   if (D < 8 || D > 256 || D % 8) { moba_set_error("prefill_fwd: head_dim must be a multiple of 8 in [8,256]"); return MOBA_ERR_ARG; }
   if (Hq < 1 || Hkv < 1 || Hq % Hkv) { moba_set_error("prefill_fwd: Hq must be a positive multiple of Hkv"); return MOBA_ERR_ARG; }
   if (R < 0 || R > 8) { moba_set_error("prefill_fwd: remote count must be in [0,8]"); return MOBA_ERR_ARG; }
-  if (Hq > 65535) { moba_set_error("prefill_fwd: too many heads"); return MOBA_ERR_ARG; }
+  if (Hq > 65535 || n_self_tiles > 65535) { moba_set_error("prefill_fwd: too many heads or self tiles"); return MOBA_ERR_ARG; }
   FwdArgs a;
   a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v;
   a.T = T; a.Hq = Hq; a.Hkv = Hkv; a.D = D; a.G = Hq / Hkv;
