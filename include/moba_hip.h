@@ -151,7 +151,7 @@ int moba_hip_paged_append(const void* k, const void* v, int dtype, int N, int Hk
 
 /* Key means of closed chunks into means [B, max_chunks, Hkv, D] (cache dtype):
  * canonical fp32 sum (64 strided partial sums, then a fixed pairwise tree),
- * / chunk.  mode 0: item i = (item_seq[i], chunk
+ * / chunk, for chunk in [1, 1024].  mode 0: item i = (item_seq[i], chunk
  * item_chunk_or_pos[i]); mode 1: item i = query row at position p, closing
  * chunk p / chunk only when (p + 1) % chunk == 0.
  * Replaces _closed_means_kernel (paged_decode.py:26-44) and _step_means
@@ -203,7 +203,7 @@ int moba_hip_decode_metadata(int* table, int table_width, int* lengths, const in
 /* Prepared-decode step prologue in ONE launch for B fixed rows: apply the
  * page-table delta, positions = lengths, lengths += 1, scatter the new token
  * k/v [B,Hkv,D] into the pool, and, for a row whose token closes its chunk,
- * write that chunk's mean (same canonical order as moba_hip_block_means).
+ * write that chunk's mean (same canonical order as moba_hip_block_means); chunk in [1, 1024].
  * Replaces _metadata + _append_kernel + _step_means
  * (prepared_decode.py:6-41, paged_decode.py:10-23). */
 int moba_hip_decode_step(int* table, int table_width, int* lengths, const int* ids,

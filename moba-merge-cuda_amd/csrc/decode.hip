@@ -80,6 +80,45 @@ __global__ void append_vec_kernel(const uint16_t* __restrict__ k, const uint16_t
 }
 
 // ------------------------------------------------------------------- means
+// Lane j's partial sums (8 dims from d0) of a chunk's keys: tokens t0 + j,
+// t0 + j + 64, ... (at most kMeansPer of them, C <= 1024), added in that order
+// (the canonical order; canon_tree then combines the 64 lanes).  All page
+// lookups, then all row loads, are issued unconditionally (addresses clamped
+// to token t0 / page offset 0) and masked after: guarded loads compiled to
+// one full wait each.  A masked token adds +0, an exact no-op on a sum that
+// starts at +0.
+constexpr int kMeansPer = 16;
+
+template <int DT, bool VEC>
+MOBA_DEV void chunk_partials(const uint16_t* __restrict__ kc, const int* __restrict__ trow, int P,
+                             int Hkv, int D, int kh, int d0, int t0, int C, int lane,
+                             float (&acc)[8]) {
+  int pg[kMeansPer];
+#pragma unroll
+  for (int k = 0; k < kMeansPer; ++k) {
+    const int j = lane + 64 * k;
+    pg[k] = trow[(t0 + (j < C ? j : 0)) / P];
+  }
+  u16x8_t x[kMeansPer];
+#pragma unroll
+  for (int k = 0; k < kMeansPer; ++k) {
+    const int j = lane + 64 * k, t = t0 + (j < C ? j : 0);
+    const int64_t off = pg[k] >= 0 ? (((int64_t)pg[k] * P + t % P) * Hkv + kh) * D + d0 : 0;
+    if constexpr (VEC) {
+      x[k] = ld8(kc + off);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[k][e] = kc[off + (d0 + e < D ? e : 0)];
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kMeansPer; ++k) {
+    const bool on = lane + 64 * k < C && pg[k] >= 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = acc[e] + (on ? to_f32<DT>(x[k][e]) : 0.0f);
+  }
+}
+
 // One wave per (item, kv head, 8 consecutive d); lane j sums tokens j, j+64,
 // ... of the chunk through the page table, then the canonical tree.
 // mode 0: item i closes chunk chunk_or_pos[i] of sequence seq[i].
@@ -108,20 +147,7 @@ __global__ __launch_bounds__(64) void means_kernel(const uint16_t* __restrict__ 
   float acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
-  for (int t = chunk * C + lane; t < (chunk + 1) * C; t += 64) {
-    const int page = trow[t / P];
-    if (page < 0) continue;  // unmapped page (caller bug): read nothing
-    const int64_t off = (((int64_t)page * P + t % P) * Hkv + kh) * D + d0;
-    if constexpr (VEC) {
-      const u16x8_t x = ld8(kc + off);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] = acc[e] + to_f32<DT>(x[e]);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (d0 + e < D) acc[e] = acc[e] + to_f32<DT>(kc[off + e]);
-    }
-  }
+  chunk_partials<DT, VEC>(kc, trow, P, Hkv, D, kh, d0, chunk * C, C, lane, acc);
   uint16_t res[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) res[e] = from_f32<DT>(canon_tree(acc[e]) / (float)C);
@@ -656,14 +682,8 @@ __global__ __launch_bounds__(256) void step_kernel(int* __restrict__ table, int 
     float acc[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
-    for (int t = chunk * C + lane; t < (chunk + 1) * C; t += 64) {
-      const int pg = trow[t / P];
-      if (pg < 0) continue;
-      const int64_t off = (((int64_t)pg * P + t % P) * Hkv + kh) * D + d0;
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (d0 + e < D) acc[e] = acc[e] + to_f32<DT>(kc[off + e]);
-    }
+    if (D % 8 == 0) chunk_partials<DT, true>(kc, trow, P, Hkv, D, kh, d0, chunk * C, C, lane, acc);
+    else chunk_partials<DT, false>(kc, trow, P, Hkv, D, kh, d0, chunk * C, C, lane, acc);
     uint16_t res[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) res[e] = from_f32<DT>(canon_tree(acc[e]) / (float)C);
@@ -733,6 +753,7 @@ extern "C" int moba_hip_block_means(const void* k_cache, int dtype, int Hkv, int
                                     void* means, int max_chunks, void* stream) {
   if (n_items <= 0) return MOBA_OK;
   if (dtype != 0 && dtype != 1) { moba_set_error("block_means: dtype must be 0 or 1"); return MOBA_ERR_ARG; }
+  if (chunk < 1 || chunk > 1024) { moba_set_error("block_means: chunk must be in [1,1024]"); return MOBA_ERR_ARG; }
   dim3 grid((unsigned)((int64_t)n_items * Hkv * ((D + 7) / 8))), block(64);
   hipStream_t st = (hipStream_t)stream;
 #define MOBA_MEANS(DT_, VEC_)                                                                   \
@@ -828,6 +849,7 @@ extern "C" int moba_hip_decode_step(int* table, int table_width, int* lengths, c
                                     int max_chunks, void* stream) {
   if (B <= 0) return MOBA_OK;
   if (dtype != 0 && dtype != 1) { moba_set_error("decode_step: dtype must be 0 or 1"); return MOBA_ERR_ARG; }
+  if (chunk < 1 || chunk > 1024) { moba_set_error("decode_step: chunk must be in [1,1024]"); return MOBA_ERR_ARG; }
   hipStream_t st = (hipStream_t)stream;
   if (dtype == 0)
     hipLaunchKernelGGL(step_kernel<0>, dim3(B), dim3(256), 0, st, table, table_width, lengths, ids,
