@@ -590,22 +590,32 @@ __global__ __launch_bounds__(64) void combine_kernel(AttnArgs a) {
   const int p = a.pos[qrow];
   const int* sel = a.selected + (int64_t)row * a.nslot;
   const int nj = a.dense ? p / a.C + 1 : a.nslot;
+  // Each slot's loads are issued together and masked after (slots below
+  // nslot are in the row's allocation, columns clamped): guarded loads
+  // compiled to one full wait each.
   float M = -INFINITY;
-  for (int j = 0; j < nj; ++j)
-    if (a.dense || sel[j] >= 0) M = fmaxf(M, a.part_ml[2 * ((int64_t)row * a.nslot + j)]);
+  for (int j = 0; j < nj; ++j) {
+    const bool on = a.dense || sel[j] >= 0;
+    const float mj = a.part_ml[2 * ((int64_t)row * a.nslot + j)];
+    M = on ? fmaxf(M, mj) : M;
+  }
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   float z = 0.0f;
   for (int j = 0; j < nj; ++j) {
-    if (!a.dense && sel[j] < 0) continue;
+    const bool on = a.dense || sel[j] >= 0;
     const int64_t entry = (int64_t)row * a.nslot + j;
-    const float wgt = a.part_ml[2 * entry + 1] * fast_exp2(a.part_ml[2 * entry] - M);
-    z += wgt;
+    const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + 2 * entry);
     const float* po = a.part_o + entry * D;
+    float o[4];
 #pragma unroll
     for (int x = 0; x < 4; ++x) {
       const int d = lane + 64 * x;
-      if (d < D) acc[x] += wgt * po[d];
+      o[x] = po[d < D ? d : 0];
     }
+    const float wgt = on ? ml.y * fast_exp2(ml.x - M) : 0.0f;
+    z += wgt;
+#pragma unroll
+    for (int x = 0; x < 4; ++x) acc[x] += (on && lane + 64 * x < D) ? wgt * o[x] : 0.0f;
   }
   const float invz = 1.0f / z;
 #pragma unroll
