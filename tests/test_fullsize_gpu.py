@@ -1,0 +1,182 @@
+"""Parity at BASELINE.json's full sizes, through checks whose cost does not
+grow with the full problem:
+
+* prefill cfg2 / cfg3 shapes: the selected blocks of every (token, head) are
+  bit-identical to the canonical C oracle; outputs, LSE and dQ of sampled rows,
+  and dK / dV of sampled keys, match FP64 restatements of the same routes; a
+  second run is bitwise identical.  The sampled-key dK / dV sum over every row
+  that attends the key (its causal rows and the expert rows that selected its
+  chunk) with that row's probabilities taken from the kernel's own LSE, which
+  the sampled-row check pins separately.
+* decode cfg4 / cfg5 shapes: prepared steps checked like the small decode
+  tests (closed-chunk means bit-equal, routes bit-equal, outputs vs FP64).
+"""
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from decode_check import check
+from helpers import TOL, oracle_route
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(T, hq, hkv, d, seed):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    q, k, v, do = (torch.randn((T, h, d), generator=g, device="cuda").to(torch.bfloat16)
+                   for h in (hq, hkv, hkv, hq))
+    return q, k, v, do
+
+
+def _run(q, k, v, do, cu, T, cfg):
+    from moba_hip.grouped_attention import moba_hip_attention
+    qr, kr, vr = (x.detach().clone().requires_grad_(True) for x in (q, k, v))
+    out, lse = moba_hip_attention(qr, kr, vr, cu, T, cfg, return_lse=True)
+    dq, dk, dv = torch.autograd.grad(out, (qr, kr, vr), grad_outputs=do)
+    torch.cuda.synchronize()
+    return out.detach(), lse.detach(), dq, dk, dv
+
+
+def _keys_of_row(s, h, G, chunk, sel_row):
+    """Global key indices attended by row (s, h): the causal prefix of its own
+    chunk, then each selected remote chunk in full."""
+    c = s // chunk
+    idx = [np.arange(c * chunk, s + 1)]
+    for cj in sel_row:
+        if cj >= 0:
+            idx.append(np.arange(cj * chunk, (cj + 1) * chunk))
+    return np.concatenate(idx)
+
+
+def _close(actual, expected, dtype, what):
+    """The north-star bounds (max-abs, mean-abs) plus a relative-L2 bound.  At
+    full size a key attended by thousands of rows gets dK / dV entries of
+    magnitude ~10, where one bf16 ulp (0.0625) already exceeds the absolute
+    bound: each entry may also deviate by 2^-7 of its magnitude (two bf16
+    roundings' worth)."""
+    diff = np.abs(actual - expected)
+    max_tol, mean_tol = TOL[dtype]
+    assert np.isfinite(actual).all(), f"{what}: non-finite"
+    excess = diff - (max_tol + 2.0 ** -7 * np.abs(expected))
+    assert excess.max() <= 0, f"{what}: max abs {diff.max():.3e} at |ref| {np.abs(expected).flat[excess.argmax()]:.3e}"
+    assert diff.mean() <= mean_tol + 2.0 ** -7 * np.abs(expected).mean(), \
+        f"{what}: mean abs {diff.mean():.3e}"
+    rel = np.linalg.norm(actual - expected) / max(np.linalg.norm(expected), 1e-30)
+    assert rel <= 1e-2, f"{what}: relative L2 {rel:.3e}"
+
+
+@pytest.mark.parametrize("T,hq,hkv,d,chunk,topk", [
+    (16384, 14, 2, 64, 2048, 3),    # cfg2
+    (32768, 32, 32, 128, 4096, 3),  # cfg3
+])
+def test_prefill_full_size(cuda_device, T, hq, hkv, d, chunk, topk):
+    from moba_hip.ops import prefill as P
+    q, k, v, do = _inputs(T, hq, hkv, d, seed=11)
+    cu = torch.tensor([0, T], device="cuda", dtype=torch.int32)
+    cfg = {"chunk_size": chunk, "topk": topk}
+    G, scale = hq // hkv, d ** -0.5
+
+    # routing: every (token, head) bit-identical to the canonical oracle
+    plan = P.get_plan([0, T], chunk, hq, hkv, d, topk, q.device)
+    rt = P.route(plan, q, k, 0)
+    sel_ref, means_ref, _, (cu_chunk, _, _, remote) = oracle_route(q, k, cu, chunk, topk, 0)
+    np.testing.assert_array_equal(rt.means.cpu().numpy().view(np.uint32),
+                                  means_ref.view(np.uint32))
+    sel = rt.sel.cpu().numpy()
+    np.testing.assert_array_equal(sel, sel_ref)
+
+    out, lse, dq, dk, dv = _run(q, k, v, do, cu, T, cfg)
+    again = _run(q, k, v, do, cu, T, cfg)
+    for a, b in zip((out, lse, dq, dk, dv), again):
+        assert torch.equal(a, b), "second run differs"
+
+    qf, kf, vf, gf = (x.double().cpu().numpy() for x in (q, k, v, do))
+    of = out.double().cpu().numpy()
+    lse_np = lse.double().cpu().numpy()
+    rng = np.random.default_rng(5)
+
+    # sampled rows: output, LSE and dQ against FP64 on the same routes
+    rows = [(int(s), int(h)) for s, h in zip(rng.integers(0, T, 48), rng.integers(0, hq, 48))]
+    rows += [(T - 1, hq - 1), (chunk, 0), (0, 0)]
+    o_got, o_ref, dq_got, dq_ref, l_got, l_ref = [], [], [], [], [], []
+    for s, h in rows:
+        kh = h // G
+        keys = _keys_of_row(s, h, G, chunk, sel[s, h])
+        sc = kf[keys, kh] @ qf[s, h] * scale
+        m = sc.max()
+        p = np.exp(sc - m)
+        z = p.sum()
+        o = p @ vf[keys, kh] / z
+        pn = p / z
+        dp = vf[keys, kh] @ gf[s, h]
+        delta = gf[s, h] @ o
+        dqr = scale * ((pn * (dp - delta)) @ kf[keys, kh])
+        o_ref.append(o), o_got.append(of[s, h])
+        l_ref.append(m + np.log(z)), l_got.append(lse_np[s, h])
+        dq_ref.append(dqr), dq_got.append(dq[s, h].double().cpu().numpy())
+    _close(np.array(o_got), np.array(o_ref), torch.bfloat16, "sampled out")
+    np.testing.assert_allclose(l_got, l_ref, atol=5e-4, rtol=2e-5)
+    _close(np.array(dq_got), np.array(dq_ref), torch.bfloat16, "sampled dq")
+
+    # sampled keys: dK / dV over every row attending the key
+    delta_all = np.einsum("thd,thd->th", gf, of)
+    dk_got, dk_ref, dv_got, dv_ref = [], [], [], []
+    keys_sampled = [(int(j), int(kh)) for j, kh in zip(rng.integers(0, T, 6),
+                                                        rng.integers(0, hkv, 6))]
+    keys_sampled += [(0, 0), (T - 1, hkv - 1)]
+    for j, kh in keys_sampled:
+        c = j // chunk
+        heads = np.arange(kh * G, (kh + 1) * G)
+        rs, hs = [], []
+        for h in heads:  # causal rows of the key's own chunk
+            s_ = np.arange(j, min((c + 1) * chunk, T))
+            rs.append(s_), hs.append(np.full(len(s_), h))
+        for h in heads:  # expert rows that selected the chunk
+            s_ = np.nonzero((sel[:, h, :] == c).any(axis=1))[0]
+            rs.append(s_), hs.append(np.full(len(s_), h))
+        rs, hs = np.concatenate(rs), np.concatenate(hs)
+        sc = np.einsum("nd,d->n", qf[rs, hs], kf[j, kh]) * scale
+        pr = np.exp(sc - lse_np[rs, hs])
+        dp = np.einsum("nd,d->n", gf[rs, hs], vf[j, kh])
+        dv_ref.append(pr @ gf[rs, hs])
+        dk_ref.append(scale * ((pr * (dp - delta_all[rs, hs])) @ qf[rs, hs]))
+        dk_got.append(dk[j, kh].double().cpu().numpy())
+        dv_got.append(dv[j, kh].double().cpu().numpy())
+    _close(np.array(dv_got), np.array(dv_ref), torch.bfloat16, "sampled dv")
+    _close(np.array(dk_got), np.array(dk_ref), torch.bfloat16, "sampled dk")
+
+
+def _decode_cache(batch, lengths, hkv, d, page, chunk, dtype, extra, seed):
+    from moba_hip import PagedKVCache
+    cache = PagedKVCache(batch, max(lengths) + extra, hkv, d, page_size=page, chunk_size=chunk,
+                         dtype=dtype)
+    pages = list(cache._layout.free_pages)
+    random.Random(seed).shuffle(pages)  # fragmented physical pool, as the benchmark uses
+    cache._layout.free_pages = tuple(pages)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    for sid, L in enumerate(lengths):
+        for lo in range(0, L, 2048):
+            n = min(2048, L - lo)
+            k = torch.randn((n, hkv, d), generator=g, device="cuda").to(dtype)
+            v = torch.randn((n, hkv, d), generator=g, device="cuda").to(dtype)
+            cache.append(k, v, sequence_ids=[sid], cu_seqlens=[0, n])
+    return cache
+
+
+@pytest.mark.parametrize("batch,hq,hkv,d,page,chunk,topk,lo,hi,dtype", [
+    (8, 12, 2, 128, 48, 512, 4, 2048, 16384, torch.bfloat16),   # cfg4
+    (32, 16, 1, 96, 64, 1024, 8, 1024, 32768, torch.float16),   # cfg5
+])
+def test_decode_full_size(cuda_device, batch, hq, hkv, d, page, chunk, topk, lo, hi, dtype):
+    rng = random.Random(3)
+    lengths = [rng.randint(lo, hi) for _ in range(batch)]
+    cache = _decode_cache(batch, lengths, hkv, d, page, chunk, dtype, 8, seed=21)
+    g = torch.Generator(device="cuda").manual_seed(22)
+    with cache.prepare_decode(list(range(batch)), hq, topk=topk) as plan:
+        for _ in range(2):
+            q = torch.randn((batch, hq, d), generator=g, device="cuda").to(dtype)
+            kn = torch.randn((batch, hkv, d), generator=g, device="cuda").to(dtype)
+            vn = torch.randn((batch, hkv, d), generator=g, device="cuda").to(dtype)
+            check(cache, plan.step(q, kn, vn), q)
