@@ -119,10 +119,14 @@ int moba_hip_prefill_fwd(const void* q, const void* k, const void* v, int dtype,
  * parts selects the launches: 1 = Delta, expert-row packing and dq
  * (query-major kernels), 2 = dk/dv (key-major kernel, needs the Delta and
  * packing of a parts-1 call), 3 = both in order.
- * kv_splits in [1,16]: each key tile's query rows are split over that many
- * workgroups (for few kv heads); when > 1, part_dkv [kv_splits*2*T*Hkv*D]
- * fp32 is a workspace and D must be a multiple of 8.
- * Deterministic: no atomics, fixed reduction order. */
+ * kv_splits in [1,16]: when > 1 the launch runs n_kv_tiles*kv_splits
+ * workgroups and a device-built schedule cuts each key tile's query-row
+ * tiles into segments of near-equal length, so heavy tiles (early chunks that
+ * many rows select) get more workgroups than light ones; part_dkv is then a
+ * workspace of moba_hip_prefill_bwd_work(n_kv_tiles, kv_splits, D) bytes and
+ * n_kv_tiles must be <= 4096.
+ * Deterministic: no atomics, fixed reduction order (the schedule is a fixed
+ * function of the expert row counts). */
 int moba_hip_prefill_bwd(const void* q, const void* k, const void* v, const void* out,
                          const void* dout, const float* lse, int dtype, int T, int Hq, int Hkv,
                          int D, float scale, const int* cu_chunk, const int* self_tiles,
@@ -132,6 +136,12 @@ int moba_hip_prefill_bwd(const void* q, const void* k, const void* v, const void
                          int max_remote_tiles, float* delta, float* part_dq, void* dq, void* dk,
                          void* dv, int parts, int kv_splits, float* part_dkv, void* pack,
                          void* stream);
+
+/* Bytes of the row-split workspace moba_hip_prefill_bwd needs for kv_splits
+ * > 1 (0 for kv_splits < 2 or bad arguments).  No counterpart in the
+ * reference, whose backward is two flash-attention calls; a shape query like
+ * moba_hip_pack_experts_work. */
+int64_t moba_hip_prefill_bwd_work(int n_kv_tiles, int kv_splits, int D);
 
 /* ----------------------------------------------------------------- decode */
 

@@ -447,7 +447,9 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
   const bool role_p = wave < 4;
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   const int D = a.D, G = a.G;
-  const int* tile = a.kv_tiles + 4 * blockIdx.x;
+  int ti, s_lo, s_hi, slot;
+  if (!kv_work(a, ti, s_lo, s_hi, slot)) return;
+  const int* tile = a.kv_tiles + 4 * ti;
   const int c = tile[0], kt0 = tile[1], f = tile[2], kh = tile[3];
   if (c < 0) return;                        // padding entry of the XCD-ordered list
   const int c_lo = a.cu_chunk[c], c_hi = a.cu_chunk[c + 1];
@@ -492,9 +494,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
     const int n_rem = e >= 0 ? a.counts[e] : 0;
     const int rbase = e >= 0 ? a.row_off[e] : 0;
     const int n_tiles = G * n_self + (n_rem + BQ - 1) / BQ;
-    // row split: workgroup y of gridDim.y takes a contiguous share of the tiles
-    const int it_lo = (int)((int64_t)n_tiles * blockIdx.y / gridDim.y);
-    const int it_hi = (int)((int64_t)n_tiles * (blockIdx.y + 1) / gridDim.y);
+    const int it_lo = s_lo, it_hi = min(s_hi, n_tiles);  // this workgroup's share
 
     auto row_of = [&](int it, int qr) -> int {  // row index s*Hq+h, or -1
       if (it < G * n_self) {
@@ -676,12 +676,10 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
       stage_barrier();
     }
 
-    // D-layout: lane holds column d = i*32 + qi, keys 8j + 4hh + r.  With a
-    // row split the fp32 partial goes to part_dkv[(split, dk|dv)] for the
-    // fixed-order reduction.
-    if (gridDim.y > 1) {
-      const int64_t n = (int64_t)a.T * a.Hkv * D;
-      float* pdst = a.part_dkv + ((int64_t)blockIdx.y * 2 + (ROLE_P ? 1 : 0)) * n;
+    // D-layout: lane holds column d = i*32 + qi, keys 8j + 4hh + r.  A row
+    // split writes fp32 partials to its slot for the fixed-order reduction.
+    if (slot >= 0) {
+      float* pdst = a.part_dkv + (int64_t)slot * kv_slot_floats(D) + (ROLE_P ? kKvTileKeys * D : 0);
 #pragma unroll
       for (int i = 0; i < NDB; ++i) {
         const int d = i * 32 + qi;
@@ -689,7 +687,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = wkey0 + 8 * (r >> 2) + 4 * hh + (r & 3);
-          if (key < c_hi) pdst[((int64_t)key * a.Hkv + kh) * D + d] = acc[i][r];
+          if (key < c_hi) pdst[(key - key0) * D + d] = acc[i][r];
         }
       }
       return;
@@ -710,27 +708,174 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
   if (role_p) body(std::true_type{}); else body(std::false_type{});
 }
 
-// dK / dV from the row-split partials, summed in split order.
-template <int DT>
-__global__ __launch_bounds__(256) void dkdv_reduce_kernel(const float* __restrict__ part, int splits,
-                                                          int64_t n4, float scale,
-                                                          uint16_t* __restrict__ dk,
-                                                          uint16_t* __restrict__ dv) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= 2 * n4) return;
-  const int which = i >= n4;  // 0 = dK, 1 = dV
-  const int64_t j = which ? i - n4 : i;
-  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < splits; ++s) {
-    const f32x4_t x = reinterpret_cast<const f32x4_t*>(part)[(int64_t)(2 * s + which) * n4 + j];
+// Row-split schedule of the key-major kernels, built on the device because
+// the expert row counts live there.  Tile t costs n_t row tiles (its causal
+// tiles for the G heads plus its expert's packed tiles, the count every
+// key-major kernel derives).  The kernel picks the smallest segment length L
+// with sum ceil(n_t / L) <= nwg, cuts each tile into that many equal
+// segments, and deals the segments, in the XCD-grouped order of the host's
+// list (its entries L % 8 == x, i.e. whole (chunk, kv head) groups per XCD),
+// to the XCDs in contiguous runs: workgroup g runs on XCD g % 8, so a run of
+// segments that share query rows stays in one L2.  One workgroup; a fixed
+// function of the counts, so the sums below keep a fixed order.
+constexpr int kSchedMaxTiles = 4096;
+
+__device__ int block_sum_1024(int v, int* red) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) acc[e] += x[e];
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  int t = 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) t += red[i];
+  return t;
+}
+
+template <int ROWS>
+__global__ __launch_bounds__(1024) void dkdv_sched_kernel(BwdArgs a, int n_kv, int nwg, int* sched,
+                                                          int* seg) {
+  __shared__ int work[kSchedMaxTiles];
+  __shared__ int first[kSchedMaxTiles + 1];
+  __shared__ int red[16];
+  const int tid = threadIdx.x;
+  const bool grouped = n_kv % 8 == 0;
+  const int ni = n_kv / 8;
+  auto tile_of = [&](int o) { return grouped ? (o % ni) * 8 + o / ni : o; };
+  int wmax = 0, wsum = 0, nvalid = 0;
+  for (int o = tid; o < n_kv; o += 1024) {
+    const int* t = a.kv_tiles + 4 * tile_of(o);
+    int n = 0;
+    if (t[0] >= 0) {
+      const int c = t[0], kt0 = t[1], f = t[2], kh = t[3];
+      const int c_hi = a.cu_chunk[c + 1], key0 = a.cu_chunk[c] + kt0;
+      const int n_self = (max(0, c_hi - key0) + ROWS - 1) / ROWS;
+      const int n_rem = (f >= 0 && a.R > 0) ? a.counts[f * a.Hkv + kh] : 0;
+      n = max(1, a.G * n_self + (n_rem + ROWS - 1) / ROWS);  // >= 1: its keys get written
+    }
+    work[o] = n;
+    wmax = max(wmax, n);
+    wsum += n;
+    nvalid += n > 0;
   }
-  const float sc = which ? 1.0f : scale;
-  u16x4_t r;
+  // sum ceil(n_t / L) lies in [W / L, W / L + valid tiles]: the answer lies in
+  // [ceil(W / nwg), ceil(W / (nwg - valid))], and max n_t always fits
+  const int W = block_sum_1024(wsum, red), nv = block_sum_1024(nvalid, red);
+  // block max through the sum helper's scratch (values are >= 0)
 #pragma unroll
-  for (int e = 0; e < 4; ++e) r[e] = from_f32<DT>(acc[e] * sc);
-  reinterpret_cast<u16x4_t*>(which ? dv : dk)[j] = r;
+  for (int o = 32; o >= 1; o >>= 1) wmax = max(wmax, __shfl_xor(wmax, o, 64));
+  __syncthreads();
+  if ((tid & 63) == 0) red[tid >> 6] = wmax;
+  __syncthreads();
+  int hi = 1;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) hi = max(hi, red[i]);
+  if (nwg > nv) hi = min(hi, max(1, (W + (nwg - nv) - 1) / (nwg - nv)));
+  int lo = min(hi, max(1, (W + nwg - 1) / nwg));
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    int cnt = 0;
+    for (int o = tid; o < n_kv; o += 1024) cnt += (work[o] + mid - 1) / mid;
+    if (block_sum_1024(cnt, red) <= nwg) hi = mid; else lo = mid + 1;
+  }
+  const int L = lo;
+  // exclusive scan of the segment counts: thread tid owns a contiguous run
+  const int per = (n_kv + 1023) / 1024;
+  const int o0 = min(n_kv, tid * per), o1 = min(n_kv, o0 + per);
+  int mine = 0;
+  for (int o = o0; o < o1; ++o) mine += (work[o] + L - 1) / L;
+  int inc = mine;  // inclusive scan over the wave, then over the waves
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(inc, o, 64);
+    if ((tid & 63) >= o) inc += y;
+  }
+  __syncthreads();
+  if ((tid & 63) == 63) red[tid >> 6] = inc;
+  __syncthreads();
+  int base = 0;
+  for (int i = 0; i < (tid >> 6); ++i) base += red[i];
+  int run = base + inc - mine;
+  for (int o = o0; o < o1; ++o) {
+    first[o] = run;
+    run += (work[o] + L - 1) / L;
+  }
+  int S = 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) S += red[i];
+  if (tid == 0) first[n_kv] = S;
+  __syncthreads();
+  for (int o = tid; o < n_kv; o += 1024) {
+    seg[2 * tile_of(o)] = first[o];
+    seg[2 * tile_of(o) + 1] = first[o + 1] - first[o];
+  }
+  for (int g = tid; g < nwg; g += 1024) {
+    int j = g;
+    bool ok = g < S;
+    if (grouped) {  // XCD x = g % 8 takes segments [ceil(x S / 8), ceil((x+1) S / 8))
+      const int x = g % 8, s0 = (x * S + 7) / 8, s1 = ((x + 1) * S + 7) / 8;
+      j = s0 + g / 8;
+      ok = j < s1;
+    }
+    int4 w = {-1, 0, 0, -1};
+    if (ok) {
+      int l = 0, h = n_kv - 1;  // last o with first[o] <= j
+      while (l < h) {
+        const int m = (l + h + 1) >> 1;
+        if (first[m] <= j) l = m; else h = m - 1;
+      }
+      const int ns = first[l + 1] - first[l], sidx = j - first[l], n = work[l];
+      w = {tile_of(l), (int)((int64_t)n * sidx / ns), (int)((int64_t)n * (sidx + 1) / ns),
+           ns > 1 ? j : -1};
+    }
+    reinterpret_cast<int4*>(sched)[g] = w;
+  }
+}
+
+// dK / dV of the split tiles: workgroups (kv tile, y) share a tile's 16-byte
+// elements, each summed over the tile's slots in slot order (tiles with one
+// slot were written by the key-major kernel itself).
+constexpr int kReduceSplit = 8;
+template <int DT>
+__global__ __launch_bounds__(256) void dkdv_reduce_kernel(BwdArgs a) {
+  const int* t = a.kv_tiles + 4 * blockIdx.x;
+  if (t[0] < 0) return;
+  const int j0 = a.kv_seg[2 * blockIdx.x], ns = a.kv_seg[2 * blockIdx.x + 1];
+  if (ns <= 1) return;
+  const int c = t[0], kh = t[3], D = a.D;
+  const int key0 = a.cu_chunk[c] + t[1];
+  const int nk = min(kKvTileKeys, a.cu_chunk[c + 1] - key0);
+  const int n4 = nk * D / 4;
+  const int64_t slot4 = kv_slot_floats(D) / 4;
+  const f32x4_t* part = reinterpret_cast<const f32x4_t*>(a.part_dkv) + j0 * slot4;
+  for (int i = blockIdx.y * 256 + threadIdx.x; i < 2 * n4; i += 256 * kReduceSplit) {
+    const int which = i >= n4;  // 0 = dK, 1 = dV
+    const int jj = which ? i - n4 : i;
+    const f32x4_t* src = part + which * (kKvTileKeys * D / 4) + jj;
+    f32x4_t acc = src[0];
+    int s = 1;
+    for (; s + 4 <= ns; s += 4) {  // four loads in flight, added in slot order
+      f32x4_t x[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) x[u] = src[(s + u) * slot4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] += x[u][e];
+    }
+    for (; s < ns; ++s) {
+      const f32x4_t x = src[s * slot4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] += x[e];
+    }
+    const float sc = which ? 1.0f : a.scale;
+    u16x4_t r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = from_f32<DT>(acc[e] * sc);
+    const int key = key0 + jj / (D / 4), d = (jj % (D / 4)) * 4;
+    *reinterpret_cast<u16x4_t*>((which ? a.dv : a.dk) + ((int64_t)key * a.Hkv + kh) * D + d) = r;
+  }
 }
 
 template <int DT, int DP>
@@ -749,18 +894,21 @@ int launch_bwd(const BwdArgs& a, int n_self, int n_kv, int max_remote, int parts
       hipLaunchKernelGGL((dq_kernel<DT, DP, false, attn_qb<DP>()>), dim3(a.G, n_self, a.Hkv), dim3(256), 0, st, a);
   }
   if ((parts & 2) && n_kv > 0) {
-    // 128 keys per workgroup in both kernels; the host's key tiles match
-    if constexpr (DP <= 128) {
-      if constexpr (DP <= 64) launch_dkdv1<DT, DP>(a, n_kv, st);
-      else launch_dkdv2<DT, DP>(a, n_kv, st);
-    } else {
-      hipLaunchKernelGGL((dkdv_kernel<DT, DP>), dim3(n_kv, a.kv_splits), dim3(512), 0, st, a);
-    }
+    // kKvTileKeys keys per workgroup in every kernel; the host's key tiles match
+    const int n_wg = n_kv * a.kv_splits;
     if (a.kv_splits > 1) {
-      const int64_t n4 = (int64_t)a.T * a.Hkv * a.D / 4;
-      hipLaunchKernelGGL(dkdv_reduce_kernel<DT>, dim3((unsigned)((2 * n4 + 255) / 256)), dim3(256), 0,
-                         st, a.part_dkv, a.kv_splits, n4, a.scale, a.dk, a.dv);
+      constexpr int rows = 32 * dkdv_qb<DP>();  // query rows per tile of every key-major kernel
+      hipLaunchKernelGGL(dkdv_sched_kernel<DP <= 128 ? 64 : rows>, dim3(1), dim3(1024), 0, st, a,
+                         n_kv, n_wg, const_cast<int*>(a.kv_sched), const_cast<int*>(a.kv_seg));
     }
+    if constexpr (DP <= 128) {
+      if constexpr (DP <= 64) launch_dkdv1<DT, DP>(a, n_wg, st);
+      else launch_dkdv2<DT, DP>(a, n_wg, st);
+    } else {
+      hipLaunchKernelGGL((dkdv_kernel<DT, DP>), dim3(n_wg), dim3(512), 0, st, a);
+    }
+    if (a.kv_splits > 1)
+      hipLaunchKernelGGL(dkdv_reduce_kernel<DT>, dim3(n_kv, kReduceSplit), dim3(256), 0, st, a);
   }
   return moba_launch_status("prefill_bwd");
 }
@@ -773,7 +921,18 @@ int dispatch_bwd(const BwdArgs& a, int n_self, int n_kv, int max_remote, int par
   return launch_bwd<DT, 256>(a, n_self, n_kv, max_remote, parts, st);
 }
 
+// Bytes of the schedule head of the row-split workspace (256-byte aligned).
+int64_t dkdv_sched_bytes(int n_kv, int splits) {
+  return ((int64_t)16 * n_kv * splits + (int64_t)8 * n_kv + 255) / 256 * 256;
+}
+
 }  // namespace
+
+extern "C" int64_t moba_hip_prefill_bwd_work(int n_kv_tiles, int kv_splits, int D) {
+  if (n_kv_tiles < 1 || kv_splits < 2 || kv_splits > 16 || D < 8 || D > 256) return 0;
+  return dkdv_sched_bytes(n_kv_tiles, kv_splits) +
+         (int64_t)n_kv_tiles * kv_splits * kv_slot_floats(D) * 4;
+}
 
 extern "C" int moba_hip_prefill_bwd(const void* q, const void* k, const void* v, const void* out,
                                     const void* dout, const float* lse, int dtype, int T, int Hq,
@@ -792,7 +951,9 @@ extern "C" int moba_hip_prefill_bwd(const void* q, const void* k, const void* v,
   if (n_self_tiles > 65535 || Hq > 65535) { moba_set_error("prefill_bwd: too many heads or self tiles"); return MOBA_ERR_ARG; }
   if (parts < 1 || parts > 3) { moba_set_error("prefill_bwd: parts must be 1 (dq), 2 (dk/dv) or 3 (both)"); return MOBA_ERR_ARG; }
   if ((int64_t)T * Hq * D * 2 >= ((int64_t)1 << 32)) { moba_set_error("prefill_bwd: q / dO must be smaller than 4 GiB (32-bit buffer offsets)"); return MOBA_ERR_ARG; }
-  if (kv_splits < 1 || kv_splits > 16 || (kv_splits > 1 && (part_dkv == nullptr || D % 8))) { moba_set_error("prefill_bwd: kv_splits must be in [1,16], with a part_dkv workspace when > 1"); return MOBA_ERR_ARG; }
+  if (kv_splits < 1 || kv_splits > 16 || (kv_splits > 1 && part_dkv == nullptr)) { moba_set_error("prefill_bwd: kv_splits must be in [1,16], with a part_dkv workspace when > 1"); return MOBA_ERR_ARG; }
+  if (kv_splits > 1 && n_kv_tiles > kSchedMaxTiles) { moba_set_error("prefill_bwd: kv_splits > 1 needs n_kv_tiles <= 4096"); return MOBA_ERR_ARG; }
+  if ((int64_t)n_kv_tiles * kv_splits > 0x7fffffff / 4) { moba_set_error("prefill_bwd: too many kv workgroups"); return MOBA_ERR_ARG; }
   BwdArgs a;
   a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v;
   a.out = (const uint16_t*)out; a.dout = (const uint16_t*)dout; a.lse = lse;
@@ -801,7 +962,14 @@ extern "C" int moba_hip_prefill_bwd(const void* q, const void* k, const void* v,
   a.cu_chunk = cu_chunk; a.self_tiles = self_tiles; a.kv_tiles = kv_tiles;
   a.sel = sel; a.R = R; a.filtered = filtered; a.E = E;
   a.tile_off = tile_off; a.row_off = row_off; a.counts = counts; a.rows = rows;
-  a.delta = delta; a.part_dq = part_dq; a.part_dkv = part_dkv; a.kv_splits = kv_splits;
+  a.delta = delta; a.part_dq = part_dq; a.kv_splits = kv_splits;
+  a.kv_sched = a.kv_seg = nullptr; a.part_dkv = nullptr;
+  if (kv_splits > 1) {  // workspace: schedule, tile slots, then the partial slots
+    char* ws = (char*)part_dkv;
+    a.kv_sched = (const int*)ws;
+    a.kv_seg = a.kv_sched + 4 * (int64_t)n_kv_tiles * kv_splits;
+    a.part_dkv = (float*)(ws + dkdv_sched_bytes(n_kv_tiles, kv_splits));
+  }
   a.dq = (uint16_t*)dq; a.dk = (uint16_t*)dk; a.dv = (uint16_t*)dv;
   a.lse2 = delta + (int64_t)T * Hq;
   a.pack_rows = (R > 0 && D <= 128) ? (int64_t)T * Hq * R : 0;

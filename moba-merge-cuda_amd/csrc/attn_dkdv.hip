@@ -61,7 +61,9 @@ __global__ __launch_bounds__(256, 1) void dkdv1_kernel(BwdArgs a) {
   const int qi = lane & 31, hh = lane >> 5;
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   const int D = a.D, G = a.G;
-  const int* tile = a.kv_tiles + 4 * blockIdx.x;
+  int ti, s_lo, s_hi, slot;
+  if (!kv_work(a, ti, s_lo, s_hi, slot)) return;
+  const int* tile = a.kv_tiles + 4 * ti;
   const int c = tile[0], kt0 = tile[1], f = tile[2], kh = tile[3];
   if (c < 0) return;                          // padding entry of the XCD-ordered list
   const int c_lo = a.cu_chunk[c], c_hi = a.cu_chunk[c + 1];
@@ -90,9 +92,7 @@ __global__ __launch_bounds__(256, 1) void dkdv1_kernel(BwdArgs a) {
   const int n_rem = e >= 0 ? a.counts[e] : 0;
   const int rbase = e >= 0 ? a.row_off[e] : 0;
   const int n_tiles = G * n_self + (n_rem + kRows - 1) / kRows;
-  // row split: workgroup y of gridDim.y takes a contiguous share of the tiles
-  const int it_lo = (int)((int64_t)n_tiles * blockIdx.y / gridDim.y);
-  const int it_hi = (int)((int64_t)n_tiles * (blockIdx.y + 1) / gridDim.y);
+  const int it_lo = s_lo, it_hi = min(s_hi, n_tiles);  // this workgroup's share
 
   // Every tile's rows are affine in the row number, so the loads need no row
   // indices: self tiles read q / dO / lse2 / delta in place (row stride Hq),
@@ -244,12 +244,10 @@ __global__ __launch_bounds__(256, 1) void dkdv1_kernel(BwdArgs a) {
   }
   wait_vmcnt<0>();  // no loads in flight when the workgroup ends
 
-  // D layout: lane holds column d = i*32 + qi, keys 8j + 4hh + r.  With a
-  // row split the fp32 partials go to part_dkv[(split, dk|dv)] for the
-  // fixed-order reduction.
-  const int64_t nkd = (int64_t)a.T * a.Hkv * D;
-  float* pk = a.part_dkv + ((int64_t)blockIdx.y * 2) * nkd;
-  float* pv = pk + nkd;
+  // D layout: lane holds column d = i*32 + qi, keys 8j + 4hh + r.  A row
+  // split writes fp32 partials to its slot for the fixed-order reduction.
+  float* pk = a.part_dkv + (int64_t)max(slot, 0) * kv_slot_floats(D);
+  float* pv = pk + kKvTileKeys * D;
 #pragma unroll
   for (int i = 0; i < NDB; ++i) {
     const int d = i * 32 + qi;
@@ -259,9 +257,9 @@ __global__ __launch_bounds__(256, 1) void dkdv1_kernel(BwdArgs a) {
       const int key = wkey0 + 8 * (r >> 2) + 4 * hh + (r & 3);
       if (key >= c_hi) continue;
       const int64_t o = ((int64_t)key * a.Hkv + kh) * D + d;
-      if (gridDim.y > 1) {
-        pk[o] = dk[i][r];
-        pv[o] = dv[i][r];
+      if (slot >= 0) {
+        pk[(key - key0) * D + d] = dk[i][r];
+        pv[(key - key0) * D + d] = dv[i][r];
       } else {
         a.dk[o] = from_f32<DT>(dk[i][r] * a.scale);
         a.dv[o] = from_f32<DT>(dv[i][r]);
@@ -272,8 +270,8 @@ __global__ __launch_bounds__(256, 1) void dkdv1_kernel(BwdArgs a) {
 
 }  // namespace
 
-template <int DT, int DP> void launch_dkdv1(const BwdArgs& a, int n_kv, hipStream_t st) {
-  hipLaunchKernelGGL((dkdv1_kernel<DT, DP>), dim3(n_kv, a.kv_splits), dim3(256), 0, st, a);
+template <int DT, int DP> void launch_dkdv1(const BwdArgs& a, int n_wg, hipStream_t st) {
+  hipLaunchKernelGGL((dkdv1_kernel<DT, DP>), dim3(n_wg), dim3(256), 0, st, a);
 }
 
 template void launch_dkdv1<0, 32>(const BwdArgs&, int, hipStream_t);

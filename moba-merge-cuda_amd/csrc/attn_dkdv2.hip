@@ -64,7 +64,9 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
   const int pair = wave & 3;
   const bool role_p = wave < 4;
   const int D = a.D, G = a.G;
-  const int* tile = a.kv_tiles + 4 * blockIdx.x;
+  int ti, s_lo, s_hi, slot;
+  if (!kv_work(a, ti, s_lo, s_hi, slot)) return;
+  const int* tile = a.kv_tiles + 4 * ti;
   const int c = tile[0], kt0 = tile[1], f = tile[2], kh = tile[3];
   if (c < 0) return;                          // padding entry of the XCD-ordered list
   const int c_lo = a.cu_chunk[c], c_hi = a.cu_chunk[c + 1];
@@ -91,9 +93,7 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
   const int n_rem = e >= 0 ? a.counts[e] : 0;
   const int rbase = e >= 0 ? a.row_off[e] : 0;
   const int n_tiles = G * n_self + (n_rem + kRows - 1) / kRows;
-  // row split: workgroup y of gridDim.y takes a contiguous share of the tiles
-  const int it_lo = (int)((int64_t)n_tiles * blockIdx.y / gridDim.y);
-  const int it_hi = (int)((int64_t)n_tiles * (blockIdx.y + 1) / gridDim.y);
+  const int it_lo = s_lo, it_hi = min(s_hi, n_tiles);  // this workgroup's share
 
   // Tile loads: self tiles read q / dO / lse2 / delta in place (row stride
   // Hq), expert tiles the packed copies (row stride 1); rows past the tile's
@@ -330,11 +330,10 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
       step(Q1, G1, L1, Q2, G2, L2, Q0, G0, L0);
     }
 
-    // D layout: lane holds column d = i*32 + qi, keys 8j + 4hh + r.  With a
-    // row split the fp32 partials go to part_dkv[(split, dk|dv)] for the
-    // fixed-order reduction.
-    const int64_t nkd = (int64_t)a.T * a.Hkv * D;
-    float* pdst = a.part_dkv + ((int64_t)blockIdx.y * 2 + (ROLE_P ? 1 : 0)) * nkd;
+    // D layout: lane holds column d = i*32 + qi, keys 8j + 4hh + r.  A row
+    // split writes fp32 partials to its slot for the fixed-order reduction.
+    float* pdst = a.part_dkv + (int64_t)max(slot, 0) * kv_slot_floats(D) +
+                  (ROLE_P ? kKvTileKeys * D : 0);
     uint16_t* dst = ROLE_P ? a.dv : a.dk;
     const float osc = ROLE_P ? 1.0f : a.scale;
 #pragma unroll
@@ -346,7 +345,7 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
         const int key = pkey0 + 8 * (r >> 2) + 4 * hh + (r & 3);
         if (key >= c_hi) continue;
         const int64_t o = ((int64_t)key * a.Hkv + kh) * D + d;
-        if (gridDim.y > 1) pdst[o] = acc[i][r];
+        if (slot >= 0) pdst[(key - key0) * D + d] = acc[i][r];
         else dst[o] = from_f32<DT>(acc[i][r] * osc);
       }
     }
@@ -356,8 +355,8 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
 
 }  // namespace
 
-template <int DT, int DP> void launch_dkdv2(const BwdArgs& a, int n_kv, hipStream_t st) {
-  hipLaunchKernelGGL((dkdv2_kernel<DT, DP>), dim3(n_kv, a.kv_splits), dim3(512), 0, st, a);
+template <int DT, int DP> void launch_dkdv2(const BwdArgs& a, int n_wg, hipStream_t st) {
+  hipLaunchKernelGGL((dkdv2_kernel<DT, DP>), dim3(n_wg), dim3(512), 0, st, a);
 }
 
 template void launch_dkdv2<0, 128>(const BwdArgs&, int, hipStream_t);

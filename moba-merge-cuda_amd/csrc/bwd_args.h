@@ -28,7 +28,14 @@ struct BwdArgs {
   float* delta;      // [T*Hq] rowsum(dO * O)
   float* lse2;       // [T*Hq] lse * log2(e)
   float* part_dq;
-  float* part_dkv;   // [kv_splits][2][T, Hkv, D] fp32 when kv_splits > 1
+  // Row-split schedule (kv_splits > 1, built on the device by
+  // dkdv_sched_kernel): kv_sched[4 * workgroup] = (kv tile, first row tile,
+  // end row tile, partial slot or -1 to write dK / dV directly), tile -1 for
+  // an idle workgroup; kv_seg[2 * kv tile] = (first slot, slots).  part_dkv
+  // holds per slot [dK | dV][128 keys][D] fp32, summed by dkdv_reduce_kernel.
+  const int* kv_sched;
+  const int* kv_seg;
+  float* part_dkv;
   int kv_splits;
   uint16_t* dq;
   uint16_t* dk;
@@ -44,7 +51,25 @@ struct BwdArgs {
 
 // Key-major dK/dV with all four products per wave (attn_dkdv.hip), head dims <= 64:
 // launches the kernel over n_kv key tiles of 128 keys x kv_splits row splits.
-template <int DT, int DP> void launch_dkdv1(const BwdArgs& a, int n_kv, hipStream_t st);
-template <int DT, int DP> void launch_dkdv2(const BwdArgs& a, int n_kv, hipStream_t st);
+template <int DT, int DP> void launch_dkdv1(const BwdArgs& a, int n_wg, hipStream_t st);
+template <int DT, int DP> void launch_dkdv2(const BwdArgs& a, int n_wg, hipStream_t st);
+
+// Keys per dK/dV workgroup (every key-major kernel) and the size of one
+// partial slot in floats.
+constexpr int kKvTileKeys = 128;
+__host__ __device__ inline int64_t kv_slot_floats(int D) { return (int64_t)2 * kKvTileKeys * D; }
+
+// Work of one dK/dV workgroup: its kv tile entry and row-tile range, and the
+// partial slot it writes (-1: dK / dV directly).  Returns false for an idle
+// workgroup.  Unscheduled launches take tile blockIdx.x and all its rows.
+__device__ inline bool kv_work(const BwdArgs& a, int& tile, int& lo, int& hi, int& slot) {
+  if (a.kv_sched == nullptr) {
+    tile = blockIdx.x; lo = 0; hi = 0x7fffffff; slot = -1;
+    return true;
+  }
+  const int* w = a.kv_sched + 4 * blockIdx.x;
+  tile = w[0]; lo = w[1]; hi = w[2]; slot = w[3];
+  return tile >= 0;
+}
 
 }  // namespace moba

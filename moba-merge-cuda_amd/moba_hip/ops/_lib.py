@@ -25,6 +25,7 @@ SIGNATURES = {
     "moba_hip_pack_experts": [_P, _I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _P, _P, _P, _P, _P, _P],
     "moba_hip_pack_experts_work": [_I, _I, _I, _I],
     "moba_hip_prefill_rows": [_I],
+    "moba_hip_prefill_bwd_work": [_I, _I, _I],
     "moba_hip_prefill_fwd": [_P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _I, _P, _I, _P, _I,
                              _P, _P, _P, _P, _I, _P, _P, _P, _P, _P],
     "moba_hip_prefill_bwd": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _I, _P, _I,
@@ -44,7 +45,8 @@ SIGNATURES = {
     "moba_hip_decode_fused": [_P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _I, _P, _P, _P, _P,
                               _P, _I, _I, _I, _I, _I, _I, _I, _P, _I, _P, _P, _P, _P, _P, _P],
 }
-_RESTYPES = {"moba_hip_last_error": ctypes.c_char_p, "moba_hip_pack_experts_work": ctypes.c_int64}
+_RESTYPES = {"moba_hip_last_error": ctypes.c_char_p, "moba_hip_pack_experts_work": ctypes.c_int64,
+             "moba_hip_prefill_bwd_work": ctypes.c_int64}
 
 _lib = None
 _lock = threading.Lock()

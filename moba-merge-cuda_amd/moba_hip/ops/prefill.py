@@ -238,8 +238,9 @@ def backward(plan: PrefillPlan, q, k, v, out, lse, dout, rt: RouteResult | None)
             plan.max_remote_tiles if R else 0, delta.data_ptr(), _lib.ptr(part_dq),
             dq.data_ptr(), dk.data_ptr(), dv.data_ptr()]
     ks = plan.kv_splits
-    part_dkv = (torch.empty(ks * 2 * T * plan.hkv * d, dtype=torch.float32, device=dev)
-                if ks > 1 else None)
+    # row-split workspace: the device-built schedule, then fp32 partial slots
+    part_dkv = (torch.empty(_lib.load().moba_hip_prefill_bwd_work(plan.n_kv_tiles, ks, d),
+                            dtype=torch.uint8, device=dev) if ks > 1 else None)
     # expert rows of q / dO / lse / delta packed contiguously for the key-major kernel
     pack = (torch.empty(T * hq * R * (4 * d + 8), dtype=torch.uint8, device=dev)
             if R and d <= 128 else None)

@@ -110,6 +110,10 @@ def test_argument_errors_are_reported_without_a_device():
         _lib.call("moba_hip_prefill_bwd", None, None, None, None, None, None, 0, 1, 1, 1, 64,
                   1.0, None, None, 0, None, 0, None, 0, None, 0, None, None, None, None, 0,
                   None, None, None, None, None, 3, 2, None, None, None)
+    with pytest.raises(_lib.MobaHipError, match="n_kv_tiles <= 4096"):
+        _lib.call("moba_hip_prefill_bwd", None, None, None, None, None, None, 0, 1, 1, 1, 64,
+                  1.0, None, None, 0, None, 4097, None, 0, None, 0, None, None, None, None, 0,
+                  None, None, None, None, None, 3, 2, 1, None, None)
     with pytest.raises(_lib.MobaHipError, match="remote count"):
         _lib.call("moba_hip_route_prefill", None, 0, 1, 1, 1, 8, None, None, 1, None, None, 9, 1,
                   None, None, None)
@@ -119,3 +123,12 @@ def test_argument_errors_are_reported_without_a_device():
     with pytest.raises(_lib.MobaHipError, match="work list"):
         _lib.call("moba_hip_paged_attention", None, 0, 1, 1, 1, 64, None, None, 1, None, 1,
                   None, None, None, None, 2, None, None, 0, 4, 1, None, None, None, None, None)
+
+
+def test_row_split_workspace_size():
+    """Schedule head (16 B per workgroup + 8 B per tile, 256-byte aligned),
+    then one [dK | dV][128 keys][D] fp32 slot per workgroup."""
+    f = _lib.load().moba_hip_prefill_bwd_work
+    assert f(256, 4, 64) == -(-(16 * 1024 + 8 * 256) // 256) * 256 + 1024 * 2 * 128 * 64 * 4
+    assert f(3, 2, 128) == 256 + 6 * 2 * 128 * 128 * 4
+    assert f(256, 1, 64) == 0 and f(0, 4, 64) == 0 and f(8, 17, 64) == 0
