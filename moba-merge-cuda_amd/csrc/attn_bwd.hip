@@ -323,6 +323,9 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a
   };
   auto run = [&](const uint16_t* Kb, const uint16_t* Vb, int it) {
     const int kt0 = k_lo + it * kBN;
+    // a causal tile wholly above this wave's rows adds exact zeros: skip it
+    // (the wave still joins the stage barriers)
+    if (!REMOTE && kt0 > s_wave0 + 32 * QB - 1) return;
     const bool need_mask = (kt0 + kBN > k_hi) || (!REMOTE && kt0 + kBN - 1 > s_wave0);
     if (need_mask) tile(Kb, Vb, it, std::true_type{}); else tile(Kb, Vb, it, std::false_type{});
   };
