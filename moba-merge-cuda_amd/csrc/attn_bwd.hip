@@ -156,15 +156,22 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a
   }
 
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
-  uint32_t voff[NDMA];
-  bool vok[NDMA];
+  // Lane l of wave w loads blocks j = (n * 4 + w) * 64 + l: row j / NB,
+  // physical block j % NB.  The row advances by 256 / NB per n, a multiple of
+  // 16 when DP <= 128, and the swizzle depends on the row mod 16 only, so
+  // every n has the same column and its offset is the n = 0 offset plus a
+  // uniform step (added per load, not held in NDMA registers).
+  constexpr bool UNI = (256 / NB) % 16 == 0;
+  uint32_t voff[UNI ? 1 : NDMA];
+  bool vok[UNI ? 1 : NDMA];
 #pragma unroll
-  for (int n = 0; n < NDMA; ++n) {
+  for (int n = 0; n < (UNI ? 1 : NDMA); ++n) {
     const int j = (n * 4 + wave_s) * 64 + lane, row = j / NB;
-    const int col = swz<DP>(row, (j % NB) * 8) - row * DP;
+    const int col = swz<DP>(row, (j % NB) * 8) - row * DP;  // swizzle is an involution
     voff[n] = (uint32_t)(((row * a.Hkv + kh) * D + col) * 2);
     vok[n] = col < D;
   }
+  const uint32_t vstep = (uint32_t)((256 / NB) * a.Hkv * D * 2);
   const int n_keys = k_hi - k_lo;
   const uint32_t nrec = (uint32_t)((((int64_t)(n_keys - 1) * a.Hkv + kh + 1) * D) * 2);
   const uint16_t* kbase = a.k + (int64_t)k_lo * a.Hkv * D;
@@ -172,11 +179,13 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a
   const uint32_t tile_bytes = (uint32_t)(kBN * a.Hkv * D * 2);
   auto dma = [&](uint16_t* Kd, uint16_t* Vd, int it) {
     const uint32_t soff = (uint32_t)it * tile_bytes;
+    const uint32_t v0 = opaque(voff[0]);
 #pragma unroll
     for (int n = 0; n < NDMA; ++n) {
-      if (vok[n]) {
-        load_lds16(make_rsrc(kbase, nrec), Kd + (n * 4 + wave_s) * 64 * 8, voff[n], soff);
-        load_lds16(make_rsrc(vbase, nrec), Vd + (n * 4 + wave_s) * 64 * 8, voff[n], soff);
+      if (vok[UNI ? 0 : n]) {
+        const uint32_t vo = UNI ? v0 + n * vstep : voff[n];
+        load_lds16(make_rsrc(kbase, nrec), Kd + (n * 4 + wave_s) * 64 * 8, vo, soff);
+        load_lds16(make_rsrc(vbase, nrec), Vd + (n * 4 + wave_s) * 64 * 8, vo, soff);
       }
     }
   };
