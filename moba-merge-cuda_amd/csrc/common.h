@@ -208,7 +208,9 @@ MOBA_DEV void load_lds16(__amdgpu_buffer_rsrc_t r, uint16_t* lds, uint32_t voff,
 }
 
 // The same LDS loads issued from inline assembly, out of the compiler's
-// sight: it inserts no waits for them (its alias tracking of LDS loads would
+// sight.  An LDS-DMA load reads M0 and needs one wait state after the SALU
+// write of M0 (the s_nop the compiler itself places in that position).  Out
+// of sight, it inserts no waits for them (its alias tracking of LDS loads would
 // otherwise wait on loads into a stage other than the one being read).  The
 // caller orders them itself: s_waitcnt vmcnt plus a barrier before the LDS is
 // read, and a barrier after the last read of a stage before it is reloaded.
@@ -217,11 +219,11 @@ MOBA_DEV uint32_t lds_addr(const void* p) {
       (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p);
 }
 MOBA_DEV void dma_lds16(__amdgpu_buffer_rsrc_t r, const void* lds, uint32_t voff, uint32_t soff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                :: "s"(lds_addr(lds)), "v"(voff), "s"(r), "s"(soff) : "memory", "m0");
 }
 MOBA_DEV void dma_lds4(__amdgpu_buffer_rsrc_t r, const void* lds, uint32_t voff, uint32_t soff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, %3 offen lds"
                :: "s"(lds_addr(lds)), "v"(voff), "s"(r), "s"(soff) : "memory", "m0");
 }
 
