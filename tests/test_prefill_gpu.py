@@ -126,3 +126,38 @@ def test_repeat_bitwise(cuda_device):
     for other in outs[1:]:
         for a, b in zip(outs[0], other):
             assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dim", [64, 128, 256])
+def test_skewed_routes_row_split(cuda_device, dim):
+    """Every query routes to chunk 0 (its keys and the queries share a strong
+    component), so chunk 0's key tiles carry almost all expert rows and the
+    device-built row-split schedule cuts them into many segments while the
+    other tiles get one each.  Gradients against FP64 on the same routes."""
+    hq, hkv, lens, chunk, topk, dtype = 8, 2, (1024,), 64, 3, torch.bfloat16
+    q, k, v, cu, ml, g = prefill_inputs(hq, hkv, dim, lens, dtype, seed=71)
+    gen = torch.Generator().manual_seed(72)
+    u = torch.randn(dim, generator=gen)
+    u = (u / u.norm() * 3.0).to(q.device)
+    q = (q.float() + u).to(dtype)
+    k = k.float()
+    k[:chunk] += u
+    k = k.to(dtype)
+    cfg = {"chunk_size": chunk, "topk": topk}
+    qr, kr, vr, out, lse, plan = _run(q, k, v, cu, ml, cfg)
+    assert plan.kv_splits > 1, "the shape must take the row-split path"
+    dq, dk, dv = torch.autograd.grad(out, (qr, kr, vr), grad_outputs=g)
+    sel, _, _, (att_chunk, _, _, _) = oracle_route(q, k, cu, chunk, topk)
+    eligible = np.arange(lens[0]) >= chunk
+    assert (sel[eligible] == 0).any(axis=-1).mean() > 0.9, "routing is not skewed"
+    qd, kd, vd, gd = (x.detach().double().cpu().numpy() for x in (q, k, v, g))
+    o_ref, l_ref = O.attention_fwd(qd, kd, vd, att_chunk, sel)
+    assert_close_stats(out, o_ref, dtype, "out")
+    dq_ref, dk_ref, dv_ref = O.attention_bwd(qd, kd, vd, gd, att_chunk, sel, l_ref)
+    for name, a, e in (("dq", dq, dq_ref), ("dk", dk, dk_ref), ("dv", dv, dv_ref)):
+        scale = max(1.0, float(np.abs(e).max()) / 4)
+        diff = np.abs(a.double().cpu().numpy() - e)
+        max_tol, mean_tol = TOL[dtype]
+        assert np.isfinite(diff).all(), name
+        assert diff.max() <= max_tol * scale, f"{name} max {diff.max():.3e} (scale {scale:.1f})"
+        assert diff.mean() <= mean_tol * scale, f"{name} mean {diff.mean():.3e}"
