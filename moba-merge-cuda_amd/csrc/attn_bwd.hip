@@ -55,26 +55,6 @@ __global__ __launch_bounds__(256) void delta_kernel(const uint16_t* __restrict__
   }
 }
 
-// ------------------------------------------------------------------- pack
-// Copies the expert rows (rows[m] >> 3 for m < row_off[E]) of q, dO, lse2 and
-// delta into contiguous packed arrays, so that the key-major kernel reads
-// every query tile with affine addresses.  One 16-byte piece per thread.
-__global__ __launch_bounds__(256) void pack_rows_kernel(BwdArgs a) {
-  const int nb = a.D / 8;
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t m = i / nb;
-  const int M = a.row_off[a.E];
-  if (m >= M) return;
-  const int b = (int)(i % nb);
-  const int64_t row = a.rows[m] >> 3;
-  st8(a.pack_q + m * a.D + b * 8, ld8(a.q + row * a.D + b * 8));
-  st8(a.pack_g + m * a.D + b * 8, ld8(a.dout + row * a.D + b * 8));
-  if (b == 0) {
-    a.pack_lse2[m] = a.lse2[row];
-    a.pack_delta[m] = a.delta[row];
-  }
-}
-
 // --------------------------------------------------------------------- dq
 // Per wave two blocks of 32 query rows; K/V tiles of 64 keys double-buffered
 // in LDS (row-major).  S^T = K Q^T and dP^T = V dO^T take K / V rows as the A
@@ -95,6 +75,7 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a
   const int D = a.D;
 
   int s[QB], h[QB], slot[QB];
+  int pidx[QB];  // packed index of an expert row (row_off order)
   bool valid[QB];
   int kh, k_lo, k_hi, s_wave0 = 0;
   if constexpr (REMOTE) {
@@ -115,6 +96,7 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a
     for (int qb = 0; qb < QB; ++qb) {
       const int local = (t - a.tile_off[e]) * (128 * QB) + wave * (32 * QB) + qb * 32 + qi;
       valid[qb] = local < cnt;
+      pidx[qb] = base + local;
       const int packed = valid[qb] ? a.rows[base + local] : 0;  // (row << 3) | j
       const int sh = packed >> 3;
       slot[qb] = sh * a.R + (packed & 7);
@@ -153,6 +135,29 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a
     }
     lse2[qb] = valid[qb] ? a.lse[row] * kLog2e : INFINITY;
     dl[qb] = valid[qb] ? a.delta[row] : 0.0f;
+  }
+  if constexpr (REMOTE && DP <= 128) {
+    // The key-major dK/dV kernel reads the expert rows packed contiguously in
+    // row_off order; this kernel holds exactly those rows, so it writes the
+    // packed q / dO / lse2 / delta (the values delta_kernel and the loads above
+    // produce) instead of a separate gather pass.
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      if (!valid[qb]) continue;
+      const int64_t m = pidx[qb];
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        const int d = ks * 16 + hh * 8;
+        if (d < D) {
+          st8(a.pack_q + m * D + d, qf[qb][ks]);
+          st8(a.pack_g + m * D + d, gf[qb][ks]);
+        }
+      }
+      if (hh == 0) {
+        a.pack_lse2[m] = lse2[qb];
+        a.pack_delta[m] = dl[qb];
+      }
+    }
   }
 
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
@@ -896,10 +901,6 @@ int launch_bwd(const BwdArgs& a, int n_self, int n_kv, int max_remote, int parts
   if (parts & 1) {
     hipLaunchKernelGGL(delta_kernel<DT>, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, st,
                        a.out, a.dout, a.lse, rows, a.D, a.delta, a.lse2);
-    if (DP <= 128 && a.pack_rows > 0) {  // expert rows for the key-major kernel
-      const int64_t pieces = a.pack_rows * (a.D / 8);
-      hipLaunchKernelGGL(pack_rows_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, st, a);
-    }
     if (max_remote > 0 && a.R > 0)
       hipLaunchKernelGGL((dq_kernel<DT, DP, true, attn_qb<DP>()>), dim3((max_remote + 7) / 8 * 8), dim3(256), 0, st, a);
     if (n_self > 0)

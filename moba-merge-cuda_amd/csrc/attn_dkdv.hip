@@ -84,7 +84,7 @@ __global__ __launch_bounds__(256, 1) void dkdv1_kernel(BwdArgs a) {
 
 
   // query tiles: G * n_self causal tiles (rows from key0 to the chunk end, for
-  // every head of the group), then the expert's rows, which the pack kernel
+  // every head of the group), then the expert's rows, which the remote dq kernel
   // laid out contiguously (row_off[e] onwards) in pack_q / pack_g / pack_ld.
   const int self_begin = key0;
   const int n_self = (max(0, c_hi - self_begin) + kRows - 1) / kRows;

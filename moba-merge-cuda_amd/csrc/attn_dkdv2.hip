@@ -25,7 +25,7 @@
 // behind role P on the P it needs, so the only synchronisation is the
 // barrier where the LDS stages rotate: P_{t-1} was written before it.  Three
 // stages hold tiles t - 1, t and t + 1 (loading).  The expert rows come
-// packed contiguously (pack_rows_kernel), so every tile is affine in the row
+// packed contiguously (written by the remote dq kernel), so every tile is affine in the row
 // number and is loaded HBM -> LDS by buffer loads issued from inline
 // assembly (the waits are placed here).
 #include <type_traits>
