@@ -214,9 +214,16 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
   auto run_block = [&](bool cur, bool prev, const uint16_t* A, const u16x8_t (&kv)[NKS],
                        f32x16_t (&sp)[QB], const uint16_t* B, const u16x8_t (&op)[QB][2],
                        f32x16_t (&acc)[NDB]) __attribute__((always_inline)) {
+    // the wave in its MFMA block issues ahead of its partner's element-wise
+    // phase on the shared SIMD
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(1);
     if (cur && prev) block(std::true_type{}, std::true_type{}, A, kv, sp, B, op, acc);
     else if (cur) block(std::true_type{}, std::false_type{}, A, kv, sp, B, op, acc);
     else if (prev) block(std::false_type{}, std::true_type{}, A, kv, sp, B, op, acc);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(0);
+    __builtin_amdgcn_sched_barrier(0);
   };
 
   auto body = [&](auto role_tag) __attribute__((always_inline)) {
