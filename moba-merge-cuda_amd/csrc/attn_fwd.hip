@@ -207,6 +207,7 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void fwd_kernel(FwdArgs 
     const int kt0 = k_lo + it * kBN;
     const uint32_t kq = opaque(kbase0), t0 = opaque(trb0), t1 = opaque(trb1);
     f32x16_t sacc[QB][2];
+    wave_prio<1>();
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
@@ -218,6 +219,7 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void fwd_kernel(FwdArgs 
         for (int qb = 0; qb < QB; ++qb) sacc[qb][kb] = mfma32<DT>(av, qf[qb][ks], sacc[qb][kb]);
       }
     }
+    wave_prio<0>();
     if constexpr (MASK) {
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb)
@@ -269,6 +271,7 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void fwd_kernel(FwdArgs 
       }
       lsum[qb] += ps;
     }
+    wave_prio<1>();
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -280,6 +283,7 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void fwd_kernel(FwdArgs 
 #pragma unroll
           for (int qb = 0; qb < QB; ++qb) oacc[qb][db] = mfma32<DT>(av, pv[qb][kb][t], oacc[qb][db]);
         }
+    wave_prio<0>();
   };
   // vmcnt(0) with the other counters left alone, then a workgroup barrier:
   // this wave's tile loads have landed, and after the barrier every wave's.

@@ -264,6 +264,15 @@ MOBA_DEV int xcd_contiguous(int L, int total) {
   return (i < per && t < total) ? t : -1;
 }
 
+// Wave issue priority (0 or 1) at a fixed point of the instruction stream: a
+// wave in an MFMA-heavy phase is set ahead of a wave in an element-wise phase
+// on the same SIMD, which keeps the matrix unit fed.
+template <int P> MOBA_DEV void wave_prio() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_setprio(P);
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 MOBA_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 template <int DT> MOBA_DEV u16x8_t pack8(const float* v) {
