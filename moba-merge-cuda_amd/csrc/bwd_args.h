@@ -1,4 +1,5 @@
-// Argument block of the prefill backward kernels (attn_bwd.hip, attn_dkdv.hip).
+// Argument block of the prefill backward kernels (attn_bwd.hip, attn_dkdv.hip,
+// attn_dkdv2.hip).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -41,7 +42,8 @@ struct BwdArgs {
   uint16_t* dk;
   uint16_t* dv;
   // Expert rows packed contiguously in row_off order for the key-major
-  // kernel: pack_rows (= T*Hq*R) rows of q, dO, lse2 and delta.
+  // kernel: pack_rows (= T*Hq*R) rows of q, dO, lse2 and delta, written by
+  // the remote dq kernel.
   uint16_t* pack_q;
   uint16_t* pack_g;
   float* pack_lse2;
@@ -49,8 +51,10 @@ struct BwdArgs {
   int64_t pack_rows;
 };
 
-// Key-major dK/dV with all four products per wave (attn_dkdv.hip), head dims <= 64:
-// launches the kernel over n_kv key tiles of 128 keys x kv_splits row splits.
+// Key-major dK/dV launches over n_wg workgroups: one per kv tile of 128 keys,
+// or, with a row-split schedule, one per schedule entry.
+// dkdv1 (attn_dkdv.hip): all four products per wave, head dims <= 64.
+// dkdv2 (attn_dkdv2.hip): wave pairs with split roles, head dims 65..128.
 template <int DT, int DP> void launch_dkdv1(const BwdArgs& a, int n_wg, hipStream_t st);
 template <int DT, int DP> void launch_dkdv2(const BwdArgs& a, int n_wg, hipStream_t st);
 
