@@ -223,8 +223,9 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a
       f32x16_t sa[QB], pa[QB];
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) { sa[qb] = zero16(); pa[qb] = zero16(); }
-      if constexpr (REMOTE) {
-        // the expert variant holds more per-row state: no room for a ring
+      if constexpr (REMOTE && DP > 64) {
+        // the expert variant holds more per-row state: above D = 64 no room
+        // for a ring (it spills); at D <= 64 it takes the ring path below
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks) {
           const uint32_t o = kb * 32 * DP * 2 + swz_b128<DP>(kq, ks);
@@ -279,7 +280,7 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a
         dsv[qb][0] = pack8<DT>(tmp);
         dsv[qb][1] = pack8<DT>(tmp + 8);
       }
-      if constexpr (REMOTE) {
+      if constexpr (REMOTE && DP > 64) {
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
 #pragma unroll
