@@ -223,7 +223,7 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a
       f32x16_t sa[QB], pa[QB];
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) { sa[qb] = zero16(); pa[qb] = zero16(); }
-      if constexpr (REMOTE && DP > 64) __builtin_amdgcn_s_setprio(1);
+      wave_prio<1>();
       if constexpr (REMOTE && DP > 64) {
         // the expert variant holds more per-row state: above D = 64 no room
         // for a ring (it spills); at D <= 64 it takes the ring path below
@@ -264,7 +264,7 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a
           __builtin_amdgcn_sched_barrier(0);
         }
       }
-      if constexpr (REMOTE && DP > 64) __builtin_amdgcn_s_setprio(0);
+      wave_prio<0>();
       u16x8_t dsv[QB][2];
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
@@ -282,7 +282,7 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a
         dsv[qb][0] = pack8<DT>(tmp);
         dsv[qb][1] = pack8<DT>(tmp + 8);
       }
-      if constexpr (REMOTE && DP > 64) __builtin_amdgcn_s_setprio(1);
+      wave_prio<1>();
       if constexpr (REMOTE && DP > 64) {
 #pragma unroll
         for (int db = 0; db < NDB; ++db)

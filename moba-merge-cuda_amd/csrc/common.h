@@ -264,14 +264,11 @@ MOBA_DEV int xcd_contiguous(int L, int total) {
   return (i < per && t < total) ? t : -1;
 }
 
-// Wave issue priority (0 or 1) at a fixed point of the instruction stream: a
-// wave in an MFMA-heavy phase is set ahead of a wave in an element-wise phase
-// on the same SIMD, which keeps the matrix unit fed.
-template <int P> MOBA_DEV void wave_prio() {
-  __builtin_amdgcn_sched_barrier(0);
-  __builtin_amdgcn_s_setprio(P);
-  __builtin_amdgcn_sched_barrier(0);
-}
+// Wave issue priority (0 or 1): a wave in an MFMA-heavy phase is set ahead of
+// a wave in an element-wise phase on the same SIMD, which keeps the matrix
+// unit fed.  No scheduling fences: the compiler keeps s_setprio in order with
+// the MFMAs and transcendental ops around it and may interleave other work.
+template <int P> MOBA_DEV void wave_prio() { __builtin_amdgcn_s_setprio(P); }
 
 MOBA_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
