@@ -93,14 +93,14 @@ int moba_hip_prefill_rows(int D);
  * block_rows = moba_hip_prefill_rows(D)) describe
  * the remote rows (R = 0: self branch only, e.g. the full-causal fallback with
  * one chunk per sequence).  max_remote_tiles bounds tile_off[E].
- * part_o [T*Hq*R, D] fp32 and part_ml [T*Hq*R, 2] fp32 (per-slot softmax
+ * part_o [T*Hq*R, D] (dtype) and part_ml [T*Hq*R, 2] fp32 (per-slot softmax
  * max and sum in the log2 domain) are workspaces.
  * out [T,Hq,D] (dtype), lse [T,Hq] fp32 natural-log global LSE. */
 int moba_hip_prefill_fwd(const void* q, const void* k, const void* v, int dtype, int T, int Hq,
                          int Hkv, int D, float scale, const int* cu_chunk, const int* self_tiles,
                          int n_self_tiles, const int* sel, int R, const int* filtered, int E,
                          const int* tile_off, const int* row_off, const int* counts,
-                         const int* rows, int max_remote_tiles, float* part_o, float* part_ml,
+                         const int* rows, int max_remote_tiles, void* part_o, float* part_ml,
                          void* out, float* lse, void* stream);
 
 /* Backward of moba_hip_prefill_fwd with the GLOBAL O and LSE.
@@ -110,7 +110,7 @@ int moba_hip_prefill_fwd(const void* q, const void* k, const void* v, int dtype,
  * lse [T,Hq] from the forward; kv_tiles[n_kv_tiles][4] = (chunk, first key,
  * filtered index or -1, kv head): one workgroup per entry, tiles of 128
  * keys; chunk -1 marks an empty entry.  delta [2*T*Hq] and
- * part_dq [T*Hq*R, D] fp32 are workspaces.  pack is a workspace of
+ * part_dq [T*Hq*R, D] (dtype) are workspaces.  pack is a workspace of
  * T*Hq*R*(4*D + 8) bytes, required when R > 0 and D <= 128 (the expert rows
  * of q, dO, lse and delta copied contiguously by the parts-1 launches and read
  * by the key-major kernel: pass the same buffer to both calls), else may be
@@ -133,7 +133,7 @@ int moba_hip_prefill_bwd(const void* q, const void* k, const void* v, const void
                          int n_self_tiles, const int* kv_tiles, int n_kv_tiles, const int* sel,
                          int R, const int* filtered, int E, const int* tile_off,
                          const int* row_off, const int* counts, const int* rows,
-                         int max_remote_tiles, float* delta, float* part_dq, void* dq, void* dk,
+                         int max_remote_tiles, float* delta, void* part_dq, void* dq, void* dk,
                          void* dv, int parts, int kv_splits, float* part_dkv, void* pack,
                          void* stream);
 

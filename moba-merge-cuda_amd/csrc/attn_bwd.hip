@@ -364,7 +364,7 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a
     if (!valid[qb]) continue;
     const int64_t row = (int64_t)s[qb] * a.Hq + h[qb];
     if constexpr (REMOTE) {
-      float* po = a.part_dq + (int64_t)slot[qb] * D;
+      uint16_t* po = a.part_dq + (int64_t)slot[qb] * D;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -374,7 +374,10 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a
             f32x4_t o;
 #pragma unroll
             for (int i = 0; i < 4; ++i) o[i] = acc[qb][db][4 * j + i] * a.scale;
-            *reinterpret_cast<f32x4_t*>(po + d0) = o;
+            u16x4_t ob;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ob[i] = from_f32<DT>(o[i]);
+            *reinterpret_cast<u16x4_t*>(po + d0) = ob;
           }
         }
     } else {
@@ -388,14 +391,14 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a
       for (int jj = 0; jj < a.R; ++jj) {
         const int64_t sl = row * a.R + jj;
         const bool on = a.sel[sl] >= 0;
-        const float* po = a.part_dq + sl * D;
-        f32x4_t o[NDB][4];
+        const uint16_t* po = a.part_dq + sl * D;
+        u16x4_t o[NDB][4];
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int d0 = db * 32 + 8 * j + 4 * hh;
-            o[db][j] = *reinterpret_cast<const f32x4_t*>(po + (d0 < D ? d0 : 0));
+            o[db][j] = *reinterpret_cast<const u16x4_t*>(po + (d0 < D ? d0 : 0));
           }
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
@@ -403,7 +406,7 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a
           for (int j = 0; j < 4; ++j) {
             const bool ok = on && db * 32 + 8 * j + 4 * hh < D;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[qb][db][4 * j + i] += ok ? o[db][j][i] : 0.0f;
+            for (int i = 0; i < 4; ++i) acc[qb][db][4 * j + i] += ok ? to_f32<DT>(o[db][j][i]) : 0.0f;
           }
       }
       uint16_t* orow = a.dq + row * D;
@@ -958,7 +961,7 @@ extern "C" int moba_hip_prefill_bwd(const void* q, const void* k, const void* v,
                                     int n_kv_tiles, const int* sel, int R, const int* filtered,
                                     int E, const int* tile_off, const int* row_off,
                                     const int* counts, const int* rows, int max_remote_tiles,
-                                    float* delta, float* part_dq, void* dq, void* dk, void* dv,
+                                    float* delta, void* part_dq, void* dq, void* dk, void* dv,
                                     int parts, int kv_splits, float* part_dkv, void* pack,
                                     void* stream) {
   if (dtype != 0 && dtype != 1) { moba_set_error("prefill_bwd: dtype must be 0 (bf16) or 1 (fp16)"); return MOBA_ERR_ARG; }
@@ -979,7 +982,7 @@ extern "C" int moba_hip_prefill_bwd(const void* q, const void* k, const void* v,
   a.cu_chunk = cu_chunk; a.self_tiles = self_tiles; a.kv_tiles = kv_tiles;
   a.sel = sel; a.R = R; a.filtered = filtered; a.E = E;
   a.tile_off = tile_off; a.row_off = row_off; a.counts = counts; a.rows = rows;
-  a.delta = delta; a.part_dq = part_dq; a.kv_splits = kv_splits;
+  a.delta = delta; a.part_dq = (uint16_t*)part_dq; a.kv_splits = kv_splits;
   a.kv_sched = a.kv_seg = nullptr; a.part_dkv = nullptr;
   if (kv_splits > 1) {  // workspace: schedule, tile slots, then the partial slots
     char* ws = (char*)part_dkv;

@@ -52,7 +52,7 @@ struct FwdArgs {
   const int* row_off;
   const int* counts;
   const int* rows;
-  float* part_o;
+  uint16_t* part_o;     // remote partial outputs, input dtype
   float* part_ml;
   uint16_t* out;
   float* lse;
@@ -318,7 +318,7 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void fwd_kernel(FwdArgs 
     if (!valid[qb]) continue;
     if constexpr (REMOTE) {
       const float inv = 1.0f / l;
-      float* po = a.part_o + (int64_t)slot[qb] * D;
+      uint16_t* po = a.part_o + (int64_t)slot[qb] * D;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -328,7 +328,10 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void fwd_kernel(FwdArgs 
             f32x4_t o;
 #pragma unroll
             for (int i = 0; i < 4; ++i) o[i] = oacc[qb][db][4 * j + i] * inv;
-            *reinterpret_cast<f32x4_t*>(po + d0) = o;
+            u16x4_t ob;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ob[i] = from_f32<DT>(o[i]);
+            *reinterpret_cast<u16x4_t*>(po + d0) = ob;
           }
         }
       // partial stored as (running max, sum) in the log2 domain: merging
@@ -360,14 +363,14 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void fwd_kernel(FwdArgs 
         const int64_t sl = row * a.R + jj;
         const int sv = a.sel[sl];
         const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + 2 * sl);
-        const float* po = a.part_o + sl * D;
-        f32x4_t o[NDB][4];
+        const uint16_t* po = a.part_o + sl * D;
+        u16x4_t o[NDB][4];
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int d0 = db * 32 + 8 * j + 4 * hh;
-            o[db][j] = *reinterpret_cast<const f32x4_t*>(po + (d0 < D ? d0 : 0));
+            o[db][j] = *reinterpret_cast<const u16x4_t*>(po + (d0 < D ? d0 : 0));
           }
         // an unselected slot's data may be stale or NaN: select, never 0 * x
         const float w = sv >= 0 ? ml.y * fast_exp2(ml.x - M2) : 0.0f;
@@ -378,7 +381,7 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void fwd_kernel(FwdArgs 
           for (int j = 0; j < 4; ++j) {
             const bool ok = sv >= 0 && db * 32 + 8 * j + 4 * hh < D;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) oacc[qb][db][4 * j + i] += ok ? w * o[db][j][i] : 0.0f;
+            for (int i = 0; i < 4; ++i) oacc[qb][db][4 * j + i] += ok ? w * to_f32<DT>(o[db][j][i]) : 0.0f;
           }
       }
       const float invz = 1.0f / z;
@@ -437,7 +440,7 @@ extern "C" int moba_hip_prefill_fwd(const void* q, const void* k, const void* v,
                                     const int* self_tiles, int n_self_tiles, const int* sel, int R,
                                     const int* filtered, int E, const int* tile_off,
                                     const int* row_off, const int* counts, const int* rows,
-                                    int max_remote_tiles, float* part_o, float* part_ml,
+                                    int max_remote_tiles, void* part_o, float* part_ml,
                                     void* out, float* lse, void* stream) {
   if (dtype != 0 && dtype != 1) { moba_set_error("prefill_fwd: dtype must be 0 (bf16) or 1 (fp16)"); return MOBA_ERR_ARG; }
   if (D < 8 || D > 256 || D % 8) { moba_set_error("prefill_fwd: head_dim must be a multiple of 8 in [8,256]"); return MOBA_ERR_ARG; }
@@ -451,7 +454,7 @@ extern "C" int moba_hip_prefill_fwd(const void* q, const void* k, const void* v,
   a.cu_chunk = cu_chunk; a.self_tiles = self_tiles;
   a.sel = sel; a.R = R; a.filtered = filtered; a.E = E;
   a.tile_off = tile_off; a.row_off = row_off; a.counts = counts; a.rows = rows;
-  a.part_o = part_o; a.part_ml = part_ml;
+  a.part_o = (uint16_t*)part_o; a.part_ml = part_ml;
   a.out = (uint16_t*)out; a.lse = lse;
   hipStream_t st = (hipStream_t)stream;
   return dtype == 0 ? dispatch_fwd<0>(a, n_self_tiles, R > 0 ? max_remote_tiles : 0, st)

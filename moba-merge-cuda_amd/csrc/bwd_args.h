@@ -28,7 +28,7 @@ struct BwdArgs {
   const int* rows;
   float* delta;      // [T*Hq] rowsum(dO * O)
   float* lse2;       // [T*Hq] lse * log2(e)
-  float* part_dq;
+  uint16_t* part_dq;  // remote dQ slots, input dtype
   // Row-split schedule (kv_splits > 1, built on the device by
   // dkdv_sched_kernel): kv_sched[4 * workgroup] = (kv tile, first row tile,
   // end row tile, partial slot or -1 to write dK / dV directly), tile -1 for

@@ -202,7 +202,7 @@ def forward(plan: PrefillPlan, q, k, v, rt: RouteResult | None):
     lse = torch.empty((T, hq), dtype=torch.float32, device=dev)
     part_o = part_ml = None
     if R:
-        part_o = torch.empty((T * hq * R, d), dtype=torch.float32, device=dev)
+        part_o = torch.empty((T * hq * R, d), dtype=q.dtype, device=dev)
         part_ml = torch.empty((T * hq * R, 2), dtype=torch.float32, device=dev)
     _lib.call("moba_hip_prefill_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(),
               DTYPE_CODE[q.dtype], T, hq, plan.hkv, d, d ** -0.5,
@@ -227,7 +227,7 @@ def backward(plan: PrefillPlan, q, k, v, out, lse, dout, rt: RouteResult | None)
     R = plan.remote
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     delta = torch.empty(2 * T * hq, dtype=torch.float32, device=dev)
-    part_dq = torch.empty((T * hq * R, d), dtype=torch.float32, device=dev) if R else None
+    part_dq = torch.empty((T * hq * R, d), dtype=q.dtype, device=dev) if R else None
     args = [q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
             dout.data_ptr(), lse.data_ptr(), DTYPE_CODE[q.dtype], T, hq, plan.hkv, d,
             d ** -0.5, plan.ptr("att_chunk"), plan.ptr("self_tiles"), plan.n_self_tiles,
