@@ -461,9 +461,13 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t G1[BQ * DP];
   __shared__ __attribute__((aligned(16))) float lse2s[2][BQ];
   __shared__ __attribute__((aligned(16))) float dels[2][BQ];
-  // P (input dtype, the same rounding dV uses) handed from role P to role D:
+  // P handed from role P to role D as a pair of input-dtype values: Px holds
+  // P rounded to the input dtype (the operand dV uses), Pr the rounding
+  // residual, so dS = (Px + Pr)(dP - delta) sees P to about 16 mantissa bits
+  // (dS from the rounded P alone doubled the dK error at D = 256).
   // [pair][qb][half][lane], 8 values per lane
   __shared__ __attribute__((aligned(16))) u16x8_t Px[4][QB][2][64];
+  __shared__ __attribute__((aligned(16))) u16x8_t Pr[4][QB][2][64];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int qi = lane & 31, hh = lane >> 5;
@@ -579,6 +583,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
       const uint16_t* A1 = ROLE_P ? Qb : Gb;
       f32x16_t sp[QB];
       u16x8_t pk[QB][2];  // role P: P as the A operand of dV += P^T dO
+      u16x8_t pr[QB][2];  // role P: rounding residual of pk
       if (!skip) {
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) sp[qb] = zero16();
@@ -614,7 +619,9 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
                   float p = fast_exp2(fmaf(sp[qb][4 * j + i], c2, -l4[i]));
                   if constexpr (MASK)
                     p = (mykey < c_hi && (!is_self || mykey <= sq0 + r0 + i)) ? p : 0.0f;
-                  pk[qb][j >> 1][(j & 1) * 4 + i] = from_f32<DT>(p);
+                  const uint16_t hi = from_f32<DT>(p);
+                  pk[qb][j >> 1][(j & 1) * 4 + i] = hi;
+                  pr[qb][j >> 1][(j & 1) * 4 + i] = from_f32<DT>(p - to_f32<DT>(hi));
                 }
               }
           };
@@ -623,6 +630,8 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
           for (int qb = 0; qb < QB; ++qb) {
             Px[pair][qb][0][lane] = pk[qb][0];
             Px[pair][qb][1][lane] = pk[qb][1];
+            Pr[pair][qb][0][lane] = pr[qb][0];
+            Pr[pair][qb][1][lane] = pr[qb][1];
           }
         }
       }
@@ -637,6 +646,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
 #pragma unroll
           for (int qb = 0; qb < QB; ++qb) {
             const u16x8_t px[2] = {Px[pair][qb][0][lane], Px[pair][qb][1][lane]};
+            const u16x8_t rx[2] = {Pr[pair][qb][0][lane], Pr[pair][qb][1][lane]};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
               const f32x4_t d4 =
@@ -644,7 +654,8 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs a) {
 #pragma unroll
               for (int i = 0; i < 4; ++i) {
                 const int r = 4 * j + i, h2 = j >> 1, x = (j & 1) * 4 + i;
-                op[qb][h2][x] = from_f32<DT>(to_f32<DT>(px[h2][x]) * (sp[qb][r] - d4[i]));
+                const float pv = to_f32<DT>(px[h2][x]) + to_f32<DT>(rx[h2][x]);
+                op[qb][h2][x] = from_f32<DT>(pv * (sp[qb][r] - d4[i]));
               }
             }
           }

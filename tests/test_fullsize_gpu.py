@@ -18,14 +18,14 @@ import pytest
 import torch
 
 from decode_check import check
-from helpers import TOL, oracle_route
+from helpers import assert_grad_close, oracle_route
 
 pytestmark = pytest.mark.gpu
 
 
-def _inputs(T, hq, hkv, d, seed):
+def _inputs(T, hq, hkv, d, seed, scale=1.0):
     g = torch.Generator(device="cuda").manual_seed(seed)
-    q, k, v, do = (torch.randn((T, h, d), generator=g, device="cuda").to(torch.bfloat16)
+    q, k, v, do = ((torch.randn((T, h, d), generator=g, device="cuda") * scale).to(torch.bfloat16)
                    for h in (hq, hkv, hkv, hq))
     return q, k, v, do
 
@@ -51,29 +51,24 @@ def _keys_of_row(s, h, G, chunk, sel_row):
 
 
 def _close(actual, expected, dtype, what):
-    """The north-star bounds (max-abs, mean-abs) plus a relative-L2 bound.  At
-    full size a key attended by thousands of rows gets dK / dV entries of
-    magnitude ~10, where one bf16 ulp (0.0625) already exceeds the absolute
-    bound: each entry may also deviate by 2^-7 of its magnitude (two bf16
-    roundings' worth)."""
-    diff = np.abs(actual - expected)
-    max_tol, mean_tol = TOL[dtype]
-    assert np.isfinite(actual).all(), f"{what}: non-finite"
-    excess = diff - (max_tol + 2.0 ** -7 * np.abs(expected))
-    assert excess.max() <= 0, f"{what}: max abs {diff.max():.3e} at |ref| {np.abs(expected).flat[excess.argmax()]:.3e}"
-    assert diff.mean() <= mean_tol + 2.0 ** -7 * np.abs(expected).mean(), \
-        f"{what}: mean abs {diff.mean():.3e}"
+    """The unscaled north-star bounds (max-abs, mean-abs) on every entry whose
+    magnitude allows them in bf16; at full size a key attended by thousands of
+    rows can get dK / dV entries of magnitude ~10, where one bf16 ulp (0.0625)
+    already exceeds the absolute bound, and those entries are held to max-abs
+    plus one ulp of |ref| (assert_grad_close).  Plus a relative-L2 bound."""
+    assert_grad_close(actual, expected, dtype, what)
     rel = np.linalg.norm(actual - expected) / max(np.linalg.norm(expected), 1e-30)
     assert rel <= 1e-2, f"{what}: relative L2 {rel:.3e}"
 
 
-@pytest.mark.parametrize("T,hq,hkv,d,chunk,topk", [
-    (16384, 14, 2, 64, 2048, 3),    # cfg2
-    (32768, 32, 32, 128, 4096, 3),  # cfg3
+@pytest.mark.parametrize("T,hq,hkv,d,chunk,topk,in_scale", [
+    (16384, 14, 2, 64, 2048, 3, 1.0),               # cfg2: N(0,1)
+    (32768, 32, 32, 128, 4096, 3, 128 ** -0.5),     # cfg3: N(0,1) / sqrt(128), as BASELINE
+    (32768, 32, 32, 128, 4096, 3, 1.0),             # cfg3 shape, unscaled (sharper softmax)
 ])
-def test_prefill_full_size(cuda_device, T, hq, hkv, d, chunk, topk):
+def test_prefill_full_size(cuda_device, T, hq, hkv, d, chunk, topk, in_scale):
     from moba_hip.ops import prefill as P
-    q, k, v, do = _inputs(T, hq, hkv, d, seed=11)
+    q, k, v, do = _inputs(T, hq, hkv, d, seed=11, scale=in_scale)
     cu = torch.tensor([0, T], device="cuda", dtype=torch.int32)
     cfg = {"chunk_size": chunk, "topk": topk}
     G, scale = hq // hkv, d ** -0.5
