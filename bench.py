@@ -209,8 +209,8 @@ def bench_decode(batch, hq, hkv, d, page, chunk, topk, lo, hi, steps, warmup, dt
         graph_wall, graph_gpu = timed(lambda: p.step(p.q, p.k, p.v, use_graph=True), steps)
         # device time of the decode work alone: back-to-back attend launches
         # (they read the cache and mutate nothing)
-        _, kernel_us = timed(lambda: p._compute(False), 50)
-        fused = p._fused is not None
+        _, kernel_us = timed(lambda: p.attend(p.q), 50)
+        fused = p.fused
     del cache
     torch.cuda.empty_cache()
     mean_bytes = float(np.mean(byte_counts))

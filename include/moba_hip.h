@@ -30,6 +30,7 @@ extern "C" {
 #define MOBA_ERR_ARG 1
 #define MOBA_ERR_LAUNCH 2
 #define MOBA_ERR_CAPACITY 3
+#define MOBA_ERR_STALE 4    /* a plan made before the pool's last change */
 
 /* Message of the last failed call on this thread. */
 const char* moba_hip_last_error(void);
@@ -257,6 +258,125 @@ int moba_hip_decode_fused(const void* q, const void* k, const void* v, int dtype
                           int R, int dense, int pos_mode, int splits, const int* sched,
                           int n_sched, int* selected, float* part_o, float* part_ml, void* out,
                           float* lse, void* stream);
+
+/* ------------------------------------------------ host page pool (CPU only)
+ *
+ * The page allocator of the paged KV cache as a host object (no device
+ * calls; usable without a GPU).  Replaces PageAllocator / IncrementalLayout
+ * (src/moba_opt/cache_layout.py:23-148) with the same observable behaviour:
+ * a LIFO free-page stack whose initial order hands out page 0 first, reset
+ * pushing a slot's pages back in logical order, transactional plans (a
+ * failed plan changes nothing; commit refuses a plan older than the pool with
+ * MOBA_ERR_STALE), and O(rows) decode steps.  Messages of MOBA_ERR_ARG are
+ * the reference's ValueError messages.  A pool is not thread-safe: callers
+ * serialise access (the Python cache holds its lock). */
+
+/* New pool of `batch` slots, table width ceil(max_seq_len / page_size). */
+int moba_pool_create(int batch, int max_seq_len, int page_size, int num_pages, int chunk,
+                     void** pool);
+void moba_pool_destroy(void* pool);
+/* Independent copy (the prepared-decode lease, cache_layout.py:108-114). */
+int moba_pool_clone(const void* pool, void** out);
+/* dst takes src's state (same shapes); views of dst stay valid
+ * (the lease's publish, cache_layout.py:143-148). */
+int moba_pool_assign(void* dst, const void* src);
+/* info[8] = batch, max_seq_len, page_size, num_pages, chunk, table width,
+ * version, free page count. */
+int moba_pool_info(const void* pool, int64_t* info);
+/* Views of the pool's storage (valid for the pool's lifetime):
+ * table [batch][width] (-1 = unmapped), lengths [batch], free stack
+ * [free count] (bottom first; the last entry is handed out next). */
+const int32_t* moba_pool_table(const void* pool);
+const int32_t* moba_pool_lengths(const void* pool);
+const int32_t* moba_pool_free(const void* pool);
+/* Reorders the free stack (a permutation of the current free pages), e.g.
+ * the seeded fragmented pool of benchmarks/benchmark_prepared.py:79-81. */
+int moba_pool_set_free(void* pool, const int32_t* pages, int n);
+/* 0 when ids[n] are valid slot ids (nonempty; unique if `unique`). */
+int moba_pool_check_ids(const void* pool, const int32_t* ids, int n, int unique);
+/* Plans appending counts[i] tokens to slot ids[i] without changing the pool
+ * (PageAllocator.plan_append, cache_layout.py:54-87): token_seq/token_pos
+ * [sum counts] (nullable), closed (slot, chunk) pairs [2*closed_cap] of the
+ * chunks the append completes, grants (slot, logical page, physical page)
+ * [3*grants_cap] taken from the top of the free stack in order, and the new
+ * length of every slot.  *version identifies the pool state planned on. */
+int moba_pool_plan_append(const void* pool, const int32_t* ids, const int32_t* counts, int n,
+                          int32_t* token_seq, int32_t* token_pos, int32_t* closed,
+                          int closed_cap, int* n_closed, int32_t* grants, int grants_cap,
+                          int* n_grants, int32_t* new_lengths, int64_t* version);
+/* Installs a plan of moba_pool_plan_append (PageAllocator.commit,
+ * cache_layout.py:89-93); MOBA_ERR_STALE unless the pool is unchanged since. */
+int moba_pool_commit_append(void* pool, const int32_t* ids, int n, const int32_t* new_lengths,
+                            const int32_t* grants, int n_grants, int64_t version);
+/* Frees the pages of slots ids[n] and empties them (PageAllocator.reset,
+ * cache_layout.py:95-103); nothing changes on an error. */
+int moba_pool_reset(void* pool, const int32_t* ids, int n);
+/* Plans one token for each slot ids[n] (IncrementalLayout.plan,
+ * cache_layout.py:116-127): positions[n] (nullable) = current lengths, and
+ * delta [2][n] = (logical page, physical page) for a row whose position
+ * starts a page, else (-1, -1); *n_grants rows take a page. */
+int moba_pool_plan_step(const void* pool, const int32_t* ids, int n, int32_t* positions,
+                        int32_t* delta, int* n_grants, int64_t* version);
+/* Installs a step plan (IncrementalLayout.commit, cache_layout.py:129-137). */
+int moba_pool_commit_step(void* pool, const int32_t* ids, int n, const int32_t* delta,
+                          int64_t version);
+
+/* ------------------------------------------------- prepared-decode driver
+ *
+ * The host side of PreparedDecode.step / .attend / .capture
+ * (src/moba_opt/prepared_decode.py:99-187) in native code: per call it plans
+ * one token per leased slot on a page-pool lease (moba_pool_clone of the
+ * cache's pool), stages the page-table delta of rows that start a page
+ * through pinned memory onto the device (no host synchronisation), refreshes
+ * the fused kernel's split schedule when rows moved by more than 1/8, launches
+ * the step (moba_hip_decode_fused, the multi-kernel sequence, or one
+ * hipGraphLaunch of the captured launches) and commits the plan.  All device
+ * buffers belong to the caller and must outlive the handle; the driver owns
+ * only pinned staging memory, events and graphs. */
+typedef struct MobaPrepDesc {
+  int dtype, rows, hq, hkv, head_dim, page_size, table_width, max_chunks, chunk, width, remote;
+  int dense;    /* 1: attend every token <= pos */
+  int fused;    /* 1: moba_hip_decode_fused; 0: step/metadata + route + paged_attention */
+  int splits;   /* fused: split cap (<= 64) */
+  int n_sched;  /* fused: workgroups of the schedule (moba_prep_sched_workgroups) */
+  void* lease;  /* page pool the driver plans on (caller-owned) */
+  const void *q, *k, *v;          /* [rows,Hq,D], [rows,Hkv,D] inputs */
+  void *k_cache, *v_cache;        /* [num_pages,page,Hkv,D] */
+  int *table, *lengths;           /* [B,table_width], [B] */
+  const int* ids_dev;             /* [rows] slot ids */
+  int *positions, *delta;         /* [rows], [2,rows] */
+  void* means;                    /* [B,max_chunks,Hkv,D] */
+  int* selected;                  /* [rows,Hq,remote+1] (null when dense) */
+  float* scores;                  /* multi-kernel route scores [rows,Hq,width] */
+  void* items; int* item_counts;  /* multi-kernel route work list */
+  float *part_o, *part_ml;        /* split (fused) or slot partials */
+  void* out; float* lse;          /* [rows,Hq,D], [rows,Hq] */
+  int* sched;                     /* fused schedule [3*n_sched + rows*Hkv] (nullable) */
+} MobaPrepDesc;
+
+/* Driver for slots ids[desc->rows]. */
+int moba_prep_create(const MobaPrepDesc* desc, const int32_t* ids, void** handle);
+void moba_prep_destroy(void* handle);
+/* One step (append != 0: a token per slot, k/v of the descriptor) or attend
+ * on `stream`; positions[rows] receives each row's position.  use_graph
+ * replays the graph of moba_prep_capture.  Input errors change nothing. */
+int moba_prep_run(void* handle, int append, int use_graph, void* stream, int32_t* positions);
+/* Captures the launches of a step / attend into a hipGraph (nothing runs;
+ * no state changes). */
+int moba_prep_capture(void* handle, int append, void* stream);
+/* Steps whose page-table delta was uploaded. */
+int64_t moba_prep_delta_uploads(const void* handle);
+/* Workgroups of a fused schedule: max(rows*hkv, min(workgroups, rows*hkv*max_splits)). */
+int moba_prep_sched_workgroups(int rows, int hkv, int workgroups, int max_splits);
+/* Split counts per (row, kv head) proportional to the expected attended
+ * tokens (largest remainders, each in [1, max_splits]) over
+ * moba_prep_sched_workgroups workgroups: entries [3*n + rows*hkv] =
+ * (row*hkv + kv head, split, splits) interleaved across rows, then the
+ * counts; splits[rows*hkv] (nullable) the counts.  No counterpart in the
+ * reference (its decode kernel has one program per (query, q head)). */
+int moba_prep_schedule(const int32_t* positions, int rows, int hkv, int group, int remote,
+                       int chunk, int dense, int workgroups, int max_splits, int32_t* entries,
+                       int32_t* splits);
 
 #ifdef __cplusplus
 }

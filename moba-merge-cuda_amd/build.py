@@ -1,6 +1,7 @@
 """Build libmoba_hip.so (gfx950) in-tree with hipcc.
 
-Every ``csrc/*.hip`` file is compiled to an object under ``_build/`` and
+Every ``csrc/*.hip`` (device code) and ``csrc/*.cpp`` (host-only runtime:
+page pool, prepared-decode driver) file is compiled to an object under ``_build/`` and
 linked into ``moba_hip/libmoba_hip.so``.  Objects are rebuilt when their
 source or any header changed.  ``python build.py`` builds; ``--force``
 rebuilds everything.
@@ -44,6 +45,9 @@ NO_VGPR_FORM = {"attn_dkdv.hip"}
 
 
 def _flags(src: Path):
+    if src.suffix == ".cpp":  # host-only sources: the host compiler, HIP runtime API only
+        return ["-O2", "-std=c++17", "-fPIC", "-Wall", "-D__HIP_PLATFORM_AMD__",
+                "-I/opt/rocm/include"]
     if src.name in NO_VGPR_FORM:
         i = FLAGS.index("-amdgpu-mfma-vgpr-form")
         return FLAGS[:i - 1] + FLAGS[i + 1:]
@@ -53,7 +57,8 @@ def _flags(src: Path):
 def _compile(src: Path, force: bool) -> Path:
     obj = OUT_DIR / (src.stem + ".o")
     if force or not obj.exists() or obj.stat().st_mtime < max(src.stat().st_mtime, _headers()):
-        cmd = [HIPCC, *_flags(src), "-c", str(src), "-o", str(obj)]
+        cc = os.environ.get("CXX", "g++") if src.suffix == ".cpp" else HIPCC
+        cmd = [cc, *_flags(src), "-c", str(src), "-o", str(obj)]
         r = subprocess.run(cmd, capture_output=True, text=True)
         if r.returncode:
             sys.stderr.write(r.stdout + r.stderr)
@@ -63,7 +68,7 @@ def _compile(src: Path, force: bool) -> Path:
 
 def build(force: bool = False, jobs: int = 8) -> Path:
     OUT_DIR.mkdir(exist_ok=True)
-    sources = sorted(CSRC.glob("*.hip"))
+    sources = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(lambda s: _compile(s, force), sources))
     newest = max(o.stat().st_mtime for o in objs)

@@ -1,0 +1,351 @@
+// Prepared-decode driver: the host side of one decode step for a fixed set
+// of cache slots, in native code.
+//
+// A step (src/moba_opt/prepared_decode.py:141-158 semantics) is:
+//   1. plan one token per leased slot on the page pool lease (positions, and
+//      the (logical, physical) page of every row that starts a page);
+//   2. if any row starts a page, stage that delta in a pinned ring slot and
+//      copy it to the device delta buffer on the stream (no host sync: a ring
+//      slot is reused only after the event of its previous copy completed);
+//   3. refresh the split schedule of the fused kernel when some row moved by
+//      more than 1/8 since the last refresh (rare; also staged through pinned
+//      memory with an event);
+//   4. launch the step: moba_hip_decode_fused (route + attention + scatter +
+//      closing mean, then the split merge), or the multi-kernel sequence for
+//      shapes the fused kernel does not take, or one hipGraphLaunch of the
+//      captured launches;
+//   5. commit the plan on the lease.
+// An "attend" is the same without the append (positions = lengths - 1).
+// Everything the device reads is a persistent buffer, so a captured graph of
+// step 4 replays any later step.  hipGraph capture happens here too (a
+// private stream in thread-local capture mode), without a framework's graph
+// object.  No call allocates device memory.
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "../../include/moba_hip.h"
+
+void moba_set_error(const char* fmt, ...);
+
+namespace {
+
+constexpr int kRing = 16;  // pinned delta staging slots
+
+struct Prepared {
+  MobaPrepDesc d;
+  std::vector<int32_t> ids;
+  int32_t* pinned = nullptr;       // [kRing][2 * rows] delta staging, then the schedule
+  int32_t* sched_pinned = nullptr;
+  hipEvent_t ring_ev[kRing] = {};
+  bool ring_used[kRing] = {};
+  hipEvent_t sched_ev = nullptr;
+  bool sched_used = false;
+  int ring_next = 0;
+  int64_t delta_uploads = 0;
+  std::vector<int32_t> delta;      // [2 * rows] of the current plan
+  std::vector<int32_t> sched_pos;  // positions of the last schedule (empty: none)
+  std::vector<int32_t> sched_splits;
+  std::vector<int32_t> sched_entries;
+  hipGraphExec_t graph[2] = {nullptr, nullptr};  // attend, step
+};
+
+int fail(int code, const char* msg) {
+  moba_set_error("%s", msg);
+  return code;
+}
+
+int hip_fail(const char* what, hipError_t e) {
+  moba_set_error("%s: %s", what, hipGetErrorString(e));
+  return MOBA_ERR_LAUNCH;
+}
+
+// Expected tokens one (row, kv head) attends at position pos: the current
+// chunk up to pos, plus the closed chunks at least one of `group` q heads
+// selects when each picks `remote` of them (expected coverage of independent
+// uniform picks).
+double expected_tokens(int pos, int group, int remote, int chunk, bool dense) {
+  if (dense) return pos + 1.0;
+  const int cur = pos / chunk, own = pos - cur * chunk + 1;
+  if (cur == 0 || remote == 0) return own;
+  const double picks = std::min(remote, cur);
+  return own + chunk * cur * (1.0 - std::pow(1.0 - picks / cur, group));
+}
+
+}  // namespace
+
+extern "C" int moba_prep_sched_workgroups(int rows, int hkv, int workgroups, int max_splits) {
+  const int r = rows * hkv;
+  return std::max(r, std::min(workgroups, r * max_splits));
+}
+
+extern "C" int moba_prep_schedule(const int32_t* positions, int rows, int hkv, int group,
+                                  int remote, int chunk, int dense, int workgroups,
+                                  int max_splits, int32_t* entries, int32_t* splits) {
+  if (rows < 1 || hkv < 1 || chunk < 1 || max_splits < 1)
+    return fail(MOBA_ERR_ARG, "prep_schedule: bad sizes");
+  const int r = rows * hkv;
+  const int total = moba_prep_sched_workgroups(rows, hkv, workgroups, max_splits);
+  std::vector<double> w(r);
+  for (int i = 0; i < r; ++i)
+    w[i] = std::max(1.0, expected_tokens(std::max(0, (int)positions[i / hkv]), group, remote,
+                                         chunk, dense != 0));
+  // largest-remainder shares of the free workgroups, each row in [1, max]
+  std::vector<int> s(r, 1), grant(r);
+  std::vector<double> share(r);
+  int free = total - r;
+  std::vector<int> active(r);
+  for (int i = 0; i < r; ++i) active[i] = i;
+  while (free > 0 && !active.empty()) {
+    double wsum = 0;
+    for (int i : active) wsum += w[i];
+    int given = 0;
+    for (int i : active) {
+      share[i] = free * w[i] / wsum;
+      grant[i] = std::min((int)share[i], max_splits - s[i]);
+      given += grant[i];
+    }
+    std::vector<int> order(active);
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) {
+      return share[a] - (int)share[a] > share[b] - (int)share[b];
+    });
+    for (int i : order) {
+      if (given >= free) break;
+      if (s[i] + grant[i] < max_splits) { ++grant[i]; ++given; }
+    }
+    for (int i : active) s[i] += grant[i];
+    free -= given;
+    std::vector<int> next;
+    for (int i : active) if (s[i] < max_splits) next.push_back(i);
+    if (given == 0) break;
+    active.swap(next);
+  }
+  // entries (row * hkv + kv head, split, splits), interleaved across rows so
+  // one row's splits spread over the launch; then the split counts
+  int e = 0, smax = 0;
+  for (int i = 0; i < r; ++i) smax = std::max(smax, s[i]);
+  for (int k = 0; k < smax; ++k)
+    for (int i = 0; i < r; ++i)
+      if (k < s[i]) { entries[3 * e] = i; entries[3 * e + 1] = k; entries[3 * e + 2] = s[i]; ++e; }
+  for (int i = 0; i < r; ++i) {
+    entries[3 * e + i] = s[i];
+    if (splits) splits[i] = s[i];
+  }
+  return MOBA_OK;
+}
+
+namespace {
+
+// Launches of one step (append) or attend on `st`; every pointer is a
+// persistent buffer of the descriptor.
+int launch(Prepared& p, bool append, hipStream_t st) {
+  const MobaPrepDesc& d = p.d;
+  if (d.fused) {
+    return moba_hip_decode_fused(d.q, append ? d.k : nullptr, append ? d.v : nullptr, d.dtype,
+                                 d.rows, d.hq, d.hkv, d.head_dim, d.k_cache, d.v_cache,
+                                 d.page_size, d.table, d.table_width, d.lengths, d.ids_dev,
+                                 d.positions, d.delta, d.means, d.max_chunks, d.chunk, d.width,
+                                 d.remote, d.dense, append ? 2 : 1, d.splits, d.sched, d.n_sched,
+                                 d.dense ? nullptr : d.selected, d.part_o, d.part_ml, d.out,
+                                 d.lse, st);
+  }
+  int rc = append ? moba_hip_decode_step(d.table, d.table_width, d.lengths, d.ids_dev,
+                                         d.positions, d.delta, d.rows, d.k, d.v, d.dtype,
+                                         d.k_cache, d.v_cache, d.page_size, d.hkv, d.head_dim,
+                                         d.chunk, d.means, d.max_chunks, st)
+                  : moba_hip_decode_metadata(d.table, d.table_width, d.lengths, d.ids_dev,
+                                             d.positions, d.delta, d.rows, 0, st);
+  if (rc) return rc;
+  if (!d.dense) {
+    rc = moba_hip_decode_route(d.q, d.dtype, d.rows, d.hq, d.hkv, d.head_dim, d.means,
+                               d.max_chunks, d.ids_dev, d.positions, d.chunk, d.width, d.remote,
+                               d.scores, d.selected, d.items, d.item_counts, st);
+    if (rc) return rc;
+  }
+  return moba_hip_paged_attention(d.q, d.dtype, d.rows, d.hq, d.hkv, d.head_dim, d.k_cache,
+                                  d.v_cache, d.page_size, d.table, d.table_width, d.lengths,
+                                  d.ids_dev, d.positions, d.dense ? nullptr : d.selected,
+                                  d.dense ? 0 : d.remote + 1, d.dense ? nullptr : d.items,
+                                  d.dense ? nullptr : d.item_counts, d.dense, d.chunk,
+                                  d.max_chunks, d.part_o, d.part_ml, d.out, d.lse, st);
+}
+
+// Stages host data in pinned memory and copies it to the device on the
+// stream; waits only if the staging slot's previous copy is still pending.
+int stage_copy(void* dev, int32_t* slot, hipEvent_t ev, bool& used, const int32_t* src, size_t n,
+               hipStream_t st) {
+  if (used) {
+    hipError_t e = hipEventSynchronize(ev);
+    if (e != hipSuccess) return hip_fail("prepared decode: staging wait", e);
+  }
+  std::memcpy(slot, src, n * sizeof(int32_t));
+  hipError_t e = hipMemcpyAsync(dev, slot, n * sizeof(int32_t), hipMemcpyHostToDevice, st);
+  if (e == hipSuccess) e = hipEventRecord(ev, st);
+  if (e != hipSuccess) return hip_fail("prepared decode: staging copy", e);
+  used = true;
+  return MOBA_OK;
+}
+
+// Refreshes the fused launch's schedule when a row moved by more than 1/8.
+int refresh_schedule(Prepared& p, const int32_t* pos, hipStream_t st) {
+  const MobaPrepDesc& d = p.d;
+  if (!d.fused || d.sched == nullptr) return MOBA_OK;
+  if (!p.sched_pos.empty()) {
+    bool near = true;
+    for (int i = 0; i < d.rows && near; ++i)
+      near = (int64_t)std::abs(pos[i] - p.sched_pos[i]) * 8 <= std::max(p.sched_pos[i], 1);
+    if (near) return MOBA_OK;
+  }
+  const int n = 3 * d.n_sched + d.rows * d.hkv;
+  std::vector<int32_t> splits(d.rows * d.hkv);
+  p.sched_entries.resize(n);
+  int rc = moba_prep_schedule(pos, d.rows, d.hkv, d.hq / d.hkv, d.remote, d.chunk, d.dense,
+                              d.n_sched, d.splits, p.sched_entries.data(), splits.data());
+  if (rc) return rc;
+  if (splits != p.sched_splits) {
+    rc = stage_copy(d.sched, p.sched_pinned, p.sched_ev, p.sched_used, p.sched_entries.data(),
+                    n, st);
+    if (rc) return rc;
+    p.sched_splits = splits;
+  }
+  p.sched_pos.assign(pos, pos + d.rows);
+  return MOBA_OK;
+}
+
+void release(Prepared* p) {
+  for (auto& g : p->graph) if (g) hipGraphExecDestroy(g);
+  for (auto& e : p->ring_ev) if (e) hipEventDestroy(e);
+  if (p->sched_ev) hipEventDestroy(p->sched_ev);
+  if (p->pinned) hipHostFree(p->pinned);
+  delete p;
+}
+
+}  // namespace
+
+extern "C" int moba_prep_create(const MobaPrepDesc* desc, const int32_t* ids, void** out) {
+  if (!desc || !ids || !out) return fail(MOBA_ERR_ARG, "prep_create: null argument");
+  *out = nullptr;
+  const MobaPrepDesc& d = *desc;
+  if (d.rows < 1 || d.hq < 1 || d.hkv < 1 || d.lease == nullptr)
+    return fail(MOBA_ERR_ARG, "prep_create: bad descriptor");
+  if (d.fused && (d.splits < 1 || d.splits > 64 || (d.sched && d.n_sched < d.rows * d.hkv)))
+    return fail(MOBA_ERR_ARG, "prep_create: bad fused schedule sizes");
+  Prepared* p = new (std::nothrow) Prepared;
+  if (!p) return fail(MOBA_ERR_ARG, "prep_create: out of host memory");
+  p->d = d;
+  p->ids.assign(ids, ids + d.rows);
+  p->delta.assign(2 * d.rows, -1);
+  const size_t ring = (size_t)kRing * 2 * d.rows;
+  const size_t sched = d.fused && d.sched ? (size_t)3 * d.n_sched + d.rows * d.hkv : 0;
+  hipError_t e = hipHostMalloc((void**)&p->pinned, (ring + sched + 1) * sizeof(int32_t),
+                               hipHostMallocDefault);
+  if (e != hipSuccess) { p->pinned = nullptr; release(p); return hip_fail("prep_create: pinned staging", e); }
+  p->sched_pinned = p->pinned + ring;
+  for (auto& ev : p->ring_ev)
+    if ((e = hipEventCreateWithFlags(&ev, hipEventDisableTiming)) != hipSuccess) {
+      release(p);
+      return hip_fail("prep_create: event", e);
+    }
+  if ((e = hipEventCreateWithFlags(&p->sched_ev, hipEventDisableTiming)) != hipSuccess) {
+    release(p);
+    return hip_fail("prep_create: event", e);
+  }
+  *out = p;
+  return MOBA_OK;
+}
+
+extern "C" void moba_prep_destroy(void* h) {
+  if (h) release(static_cast<Prepared*>(h));
+}
+
+extern "C" int64_t moba_prep_delta_uploads(const void* h) {
+  return h ? static_cast<const Prepared*>(h)->delta_uploads : -1;
+}
+
+extern "C" int moba_prep_run(void* h, int append, int use_graph, void* stream,
+                             int32_t* positions) {
+  Prepared* p = static_cast<Prepared*>(h);
+  if (!p) return fail(MOBA_ERR_ARG, "prep_run: null handle");
+  const MobaPrepDesc& d = p->d;
+  hipStream_t st = (hipStream_t)stream;
+  hipGraphExec_t g = p->graph[append ? 1 : 0];
+  if (use_graph && !g)
+    return fail(MOBA_ERR_ARG, append ? "capture('step') first" : "capture('attend') first");
+  int64_t version = 0;
+  int grants = 0;
+  int rc;
+  if (append) {
+    rc = moba_pool_plan_step(d.lease, p->ids.data(), d.rows, positions, p->delta.data(), &grants,
+                             &version);
+    if (rc) return rc;
+  } else {
+    const int32_t* len = moba_pool_lengths(d.lease);
+    for (int i = 0; i < d.rows; ++i) {
+      positions[i] = len[p->ids[i]] - 1;
+      if (positions[i] < 0) return fail(MOBA_ERR_ARG, "query positions must refer to cached tokens");
+    }
+  }
+  if (grants) {
+    const int slot = p->ring_next;
+    p->ring_next = (slot + 1) % kRing;
+    rc = stage_copy(d.delta, p->pinned + (size_t)slot * 2 * d.rows, p->ring_ev[slot],
+                    p->ring_used[slot], p->delta.data(), 2 * (size_t)d.rows, st);
+    if (rc) return rc;
+    ++p->delta_uploads;
+  }
+  if ((rc = refresh_schedule(*p, positions, st))) return rc;
+  if (use_graph) {
+    hipError_t e = hipGraphLaunch(g, st);
+    if (e != hipSuccess) return hip_fail("prepared decode: graph launch", e);
+  } else if ((rc = launch(*p, append != 0, st))) {
+    return rc;
+  }
+  if (append) return moba_pool_commit_step(d.lease, p->ids.data(), d.rows, p->delta.data(), version);
+  return MOBA_OK;
+}
+
+extern "C" int moba_prep_capture(void* h, int append, void* stream) {
+  Prepared* p = static_cast<Prepared*>(h);
+  if (!p) return fail(MOBA_ERR_ARG, "prep_capture: null handle");
+  hipGraphExec_t& slot = p->graph[append ? 1 : 0];
+  if (slot) return fail(MOBA_ERR_ARG, "graph already captured");
+  const MobaPrepDesc& d = p->d;
+  // the schedule the replays read must be valid before the first replay
+  std::vector<int32_t> pos(d.rows);
+  const int32_t* len = moba_pool_lengths(d.lease);
+  for (int i = 0; i < d.rows; ++i) pos[i] = std::max(0, len[p->ids[i]] - (append ? 0 : 1));
+  hipStream_t user = (hipStream_t)stream;
+  int rc = refresh_schedule(*p, pos.data(), user);
+  if (rc) return rc;
+  hipStream_t cs = nullptr;
+  hipError_t e = hipStreamCreateWithFlags(&cs, hipStreamNonBlocking);
+  if (e != hipSuccess) return hip_fail("prep_capture: stream", e);
+  // the capture stream starts after the user stream's pending work
+  hipEvent_t ev = nullptr;
+  e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventRecord(ev, user);
+  if (e == hipSuccess) e = hipStreamWaitEvent(cs, ev, 0);
+  hipGraph_t graph = nullptr;
+  if (e == hipSuccess) e = hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
+  if (e == hipSuccess) {
+    rc = launch(*p, append != 0, cs);
+    hipError_t e2 = hipStreamEndCapture(cs, &graph);
+    if (rc == MOBA_OK && e2 != hipSuccess) e = e2;
+  }
+  if (e == hipSuccess && rc == MOBA_OK) e = hipGraphInstantiate(&slot, graph, nullptr, nullptr, 0);
+  if (e == hipSuccess && rc == MOBA_OK) e = hipGraphUpload(slot, user);
+  if (graph) hipGraphDestroy(graph);
+  if (ev) hipEventDestroy(ev);
+  hipStreamDestroy(cs);
+  if (rc) return rc;
+  if (e != hipSuccess) {
+    if (slot) { hipGraphExecDestroy(slot); slot = nullptr; }
+    return hip_fail("prep_capture", e);
+  }
+  return MOBA_OK;
+}

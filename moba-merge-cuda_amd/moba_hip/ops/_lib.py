@@ -15,6 +15,8 @@ LIB_PATH = Path(__file__).resolve().parents[1] / "libmoba_hip.so"
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _F = ctypes.c_float
+_L = ctypes.c_int64
+_PP = ctypes.POINTER(ctypes.c_void_p)
 
 # name -> argtypes (restype int unless listed in _RESTYPES)
 SIGNATURES = {
@@ -44,8 +46,35 @@ SIGNATURES = {
     "moba_hip_decode_fused_supported": [_I, _I, _I, _I, _I],
     "moba_hip_decode_fused": [_P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _I, _P, _P, _P, _P,
                               _P, _I, _I, _I, _I, _I, _I, _I, _P, _I, _P, _P, _P, _P, _P, _P],
+    # host page pool (CPU only)
+    "moba_pool_create": [_I, _I, _I, _I, _I, _PP],
+    "moba_pool_destroy": [_P],
+    "moba_pool_clone": [_P, _PP],
+    "moba_pool_assign": [_P, _P],
+    "moba_pool_info": [_P, _P],
+    "moba_pool_table": [_P],
+    "moba_pool_lengths": [_P],
+    "moba_pool_free": [_P],
+    "moba_pool_set_free": [_P, _P, _I],
+    "moba_pool_check_ids": [_P, _P, _I, _I],
+    "moba_pool_plan_append": [_P, _P, _P, _I, _P, _P, _P, _I, _P, _P, _I, _P, _P, _P],
+    "moba_pool_commit_append": [_P, _P, _I, _P, _P, _I, _L],
+    "moba_pool_reset": [_P, _P, _I],
+    "moba_pool_plan_step": [_P, _P, _I, _P, _P, _P, _P],
+    "moba_pool_commit_step": [_P, _P, _I, _P, _L],
+    # prepared-decode driver
+    "moba_prep_create": [_P, _P, _PP],
+    "moba_prep_destroy": [_P],
+    "moba_prep_run": [_P, _I, _I, _P, _P],
+    "moba_prep_capture": [_P, _I, _P],
+    "moba_prep_delta_uploads": [_P],
+    "moba_prep_sched_workgroups": [_I, _I, _I, _I],
+    "moba_prep_schedule": [_P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P],
 }
-_RESTYPES = {"moba_hip_last_error": ctypes.c_char_p, "moba_hip_pack_experts_work": ctypes.c_int64,
+_I32P = ctypes.POINTER(ctypes.c_int32)
+_RESTYPES = {"moba_pool_destroy": None, "moba_prep_destroy": None,
+             "moba_prep_delta_uploads": ctypes.c_int64, "moba_pool_table": _I32P, "moba_pool_lengths": _I32P,
+             "moba_pool_free": _I32P, "moba_hip_last_error": ctypes.c_char_p, "moba_hip_pack_experts_work": ctypes.c_int64,
              "moba_hip_prefill_bwd_work": ctypes.c_int64}
 
 _lib = None
@@ -54,6 +83,10 @@ _lock = threading.Lock()
 
 class MobaHipError(RuntimeError):
     pass
+
+
+MOBA_ERR_ARG = 1
+MOBA_ERR_STALE = 4
 
 
 def load():

@@ -115,75 +115,45 @@ def expected_union_tokens(pos, group, remote, chunk, dense=False) -> float:
 
 def sched_workgroups(nq, hkv, workgroups=SCHED_WORKGROUPS, max_splits=SCHED_MAX_SPLITS) -> int:
     """Grid size of a scheduled launch: fixed for a given batch shape."""
-    rows = nq * hkv
-    return max(rows, min(workgroups, rows * max_splits))
+    return _lib.load().moba_prep_sched_workgroups(nq, hkv, workgroups, max_splits)
 
 
 def fused_schedule(positions, hkv, group, remote, chunk, dense=False,
                    workgroups=SCHED_WORKGROUPS, max_splits=SCHED_MAX_SPLITS):
-    """Split counts per (row, kv head) proportional to the expected attended
-    tokens (largest remainders, each in [1, max_splits]) over exactly
-    ``sched_workgroups`` workgroups.  Returns (schedule int32 list for
-    moba_hip_decode_fused: the workgroup entries (row * hkv + kv head, split,
-    splits of that row), interleaved across rows, then the split counts;
-    the split counts; the number of workgroups)."""
+    """The split schedule the prepared-decode driver uploads (computed by
+    ``moba_prep_schedule``): split counts per (row, kv head) proportional to
+    the expected attended tokens (``expected_union_tokens``; largest
+    remainders, each in [1, max_splits]) over exactly ``sched_workgroups``
+    workgroups.  Returns (schedule int32 list: the workgroup entries
+    (row * hkv + kv head, split, splits of that row) interleaved across rows,
+    then the split counts; the split counts; the number of workgroups)."""
+    import numpy as np
     rows = len(positions) * hkv
     total = sched_workgroups(len(positions), hkv, workgroups, max_splits)
-    weights = []
-    for p in positions:
-        w = expected_union_tokens(max(0, int(p)), group, remote, chunk, dense)
-        weights += [max(w, 1.0)] * hkv
-    splits = [1] * rows
-    free = total - rows
-    active = list(range(rows))
-    while free > 0 and active:
-        wsum = sum(weights[i] for i in active)
-        share = {i: free * weights[i] / wsum for i in active}
-        grant = {i: min(int(share[i]), max_splits - splits[i]) for i in active}
-        given = sum(grant.values())
-        for i in sorted(active, key=lambda i: share[i] - int(share[i]), reverse=True):
-            if given >= free:
-                break
-            if splits[i] + grant[i] < max_splits:
-                grant[i] += 1
-                given += 1
-        for i in active:
-            splits[i] += grant[i]
-        free -= given
-        active = [i for i in active if splits[i] < max_splits]
-    entries = []
-    for sidx in range(max(splits)):  # interleave rows across the launch
-        for r in range(rows):
-            if sidx < splits[r]:
-                entries += [r, sidx, splits[r]]
-    return entries + splits, splits, total
+    pos = np.asarray(positions, dtype=np.int32)
+    entries = np.zeros(3 * total + rows, dtype=np.int32)
+    splits = np.zeros(rows, dtype=np.int32)
+    _lib.call("moba_prep_schedule", pos.ctypes.data, len(positions), hkv, group, remote, chunk,
+              int(dense), workgroups, max_splits, entries.ctypes.data, splits.ctypes.data)
+    return entries.tolist(), splits.tolist(), total
 
 
 class FusedWork:
-    """Persistent workspaces of ``fused``: the split partials, and with
-    ``scheduled`` a device schedule of ``sched_workgroups`` workgroups (see
-    ``fused_schedule``) that the owner refreshes between launches."""
-    __slots__ = ("splits", "part_o", "part_ml", "sched", "sched_host", "n_sched", "sched_splits")
+    """Workspaces of ``fused``: the split partials, and with ``scheduled`` a
+    device schedule of ``sched_workgroups`` workgroups (see
+    ``fused_schedule``) that the prepared-decode driver keeps current."""
+    __slots__ = ("splits", "part_o", "part_ml", "sched", "n_sched")
 
     def __init__(self, nq, hq, hkv, d, device, splits=None, scheduled=False):
         self.splits = splits or (SCHED_MAX_SPLITS if scheduled else fused_splits(nq, hkv))
         n = nq * hq * self.splits
         self.part_o = torch.empty((n, d), dtype=torch.float32, device=device)
         self.part_ml = torch.empty((n, 2), dtype=torch.float32, device=device)
-        self.sched = self.sched_host = self.sched_splits = None
-        self.n_sched = 0
+        self.sched, self.n_sched = None, 0
         if scheduled:
             self.n_sched = sched_workgroups(nq, hkv, max_splits=self.splits)
-            size = 3 * self.n_sched + nq * hkv
-            self.sched = torch.zeros(size, dtype=torch.int32, device=device)
-            self.sched_host = torch.zeros(size, dtype=torch.int32, pin_memory=True)
-
-    def set_schedule(self, entries, splits):
-        """Uploads a schedule of n_sched workgroups (synchronous tiny copy)."""
-        assert len(entries) == len(self.sched_host)
-        self.sched_host.copy_(torch.tensor(entries, dtype=torch.int32))
-        self.sched.copy_(self.sched_host, non_blocking=False)
-        self.sched_splits = list(splits)
+            self.sched = torch.zeros(3 * self.n_sched + nq * hkv, dtype=torch.int32,
+                                     device=device)
 
 
 def fused_args(q, k, v, kc, vc, table, lengths, ids, positions, delta, means, chunk, width,
@@ -199,33 +169,10 @@ def fused_args(q, k, v, kc, vc, table, lengths, ids, positions, delta, means, ch
             work.part_o.data_ptr(), work.part_ml.data_ptr(), out.data_ptr(), lse.data_ptr())
 
 
-def launch_fused(args, stream):
-    _lib.call("moba_hip_decode_fused", *args, stream)
-
-
-class FusedLauncher:
-    """``moba_hip_decode_fused`` with its arguments converted to ctypes values
-    once (every pointer is a persistent workspace), so a launch converts only
-    the stream."""
-    __slots__ = ("fn", "args", "err")
-
-    def __init__(self, args):
-        lib = _lib.load()
-        self.fn = lib.moba_hip_decode_fused
-        self.err = lib.moba_hip_last_error
-        types = self.fn.argtypes[:-1]
-        self.args = tuple(None if a is None else t(a) for t, a in zip(types, args))
-
-    def __call__(self, stream):
-        rc = self.fn(*self.args, stream)
-        if rc != 0:
-            msg = self.err().decode(errors="replace")
-            raise _lib.MobaHipError(f"moba_hip_decode_fused failed ({rc}): {msg}")
-
-
 def fused(q, k, v, kc, vc, table, lengths, ids, positions, delta, means, chunk, width, remote,
           dense, pos_mode, selected, work: FusedWork, out, lse):
     """One-launch decode (route + attention; step mode also appends)."""
-    launch_fused(fused_args(q, k, v, kc, vc, table, lengths, ids, positions, delta, means, chunk,
-                            width, remote, dense, pos_mode, selected, work, out, lse),
-                 _lib.stream_of(q.device))
+    _lib.call("moba_hip_decode_fused",
+              *fused_args(q, k, v, kc, vc, table, lengths, ids, positions, delta, means, chunk,
+                          width, remote, dense, pos_mode, selected, work, out, lse),
+              _lib.stream_of(q.device))

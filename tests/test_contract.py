@@ -85,7 +85,7 @@ def test_decode_mode_contract(mode, topk):
 
 def _declared_symbols():
     text = (ROOT / "include" / "moba_hip.h").read_text()
-    return sorted(set(re.findall(r"\b(moba_hip_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(moba_(?:hip|pool|prep)_\w+)\s*\(", text)))
 
 
 def test_library_exports_every_declared_symbol():
