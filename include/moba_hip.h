@@ -259,6 +259,24 @@ int moba_hip_decode_fused(const void* q, const void* k, const void* v, int dtype
                           int n_sched, int* selected, float* part_o, float* part_ml, void* out,
                           float* lse, void* stream);
 
+/* Decode attention for callers that cannot allocate (code under hipGraph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference.  Same as moba_hip_decode_fused with
+ * pos_mode 0 (positions given; nothing in the cache changes) and the uniform
+ * split count S = clamp(ceil(512 / (Nq*Hkv)), 1, 64), but the split partials
+ * live in a static per-device scratch array of 8 MiB instead of caller
+ * workspaces: calls needing more than Nq*Hq*S*(D+2)*4 (+256) bytes fail
+ * with MOBA_ERR_CAPACITY before launching anything.  It calls no allocating
+ * routine.  Every call on a device shares that device's scratch: calls that
+ * overlap on one device (different streams, or different host threads)
+ * race; calls serialised on one stream do not. */
+int moba_hip_decode_attend_noalloc(const void* q, int dtype, int Nq, int Hq, int Hkv, int D,
+                                   const void* k_cache, const void* v_cache, int page_size,
+                                   const int* table, int table_width, const int* lengths,
+                                   const int* ids, const int* positions, const void* means,
+                                   int max_chunks, int chunk, int width, int R, int dense,
+                                   int* selected, void* out, float* lse, void* stream);
+
 /* ------------------------------------------------ host page pool (CPU only)
  *
  * The page allocator of the paged KV cache as a host object (no device

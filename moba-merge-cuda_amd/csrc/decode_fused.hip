@@ -26,6 +26,8 @@
 // workgroup waits for the scatter); split 0 scatters them and applies the
 // page-table delta, the last split computes the closing chunk mean, and the
 // merge advances the row's position and length.
+#include <mutex>
+
 #include "common.h"
 #include "../../include/moba_hip.h"
 
@@ -675,6 +677,16 @@ int dispatch_fused(const FusedArgs& a, int splits, size_t dyn, hipStream_t st) {
 
 }  // namespace
 
+namespace {
+// Uniform split count of an unscheduled launch: about two workgroups per CU
+// over the grid (the host wrapper's default, fused_splits in ops/decode.py).
+int uniform_splits(int Nq, int Hkv) {
+  const int64_t rows = (int64_t)Nq * Hkv;
+  if (rows < 1) return 1;
+  return (int)std::max<int64_t>(1, std::min<int64_t>(64, (512 + rows - 1) / rows));
+}
+}  // namespace
+
 extern "C" int moba_hip_decode_fused_supported(int Hq, int Hkv, int D, int width, int table_width) {
   if (Hkv < 1 || Hq % Hkv || Hq / Hkv > 16 || D % 8 || D < 8 || D > 256) return 0;
   if (table_width < 1 || table_width > kTblMax) return 0;
@@ -715,4 +727,72 @@ extern "C" int moba_hip_decode_fused(const void* q, const void* k, const void* v
   const size_t dyn = fused_route_lds(a.G, width);
   hipStream_t st = (hipStream_t)stream;
   return dtype == 0 ? dispatch_fused<0>(a, splits, dyn, st) : dispatch_fused<1>(a, splits, dyn, st);
+}
+
+// ---------------------------------------------------------------- no-alloc
+// Split partials of moba_hip_decode_attend_noalloc live in this file-scope
+// device array instead of caller workspaces.  Host code never passes the
+// array's name to a kernel: each device's copy is located once with
+// hipGetSymbolAddress (with that device current) and that address is used.
+namespace {
+constexpr size_t kNoAllocScratchBytes = size_t(8) << 20;
+constexpr int kMaxDevices = 64;
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Address of the current device's scratch array (resolved once per device).
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) { moba_set_error("decode_attend_noalloc: hipGetDevice: %s", hipGetErrorString(e)); return MOBA_ERR_LAUNCH; }
+  if (dev < 0 || dev >= kMaxDevices) { moba_set_error("decode_attend_noalloc: device %d out of range", dev); return MOBA_ERR_ARG; }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      moba_set_error("decode_attend_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
+      return MOBA_ERR_LAUNCH;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MOBA_OK;
+}
+}  // namespace
+
+extern "C" int moba_hip_decode_attend_noalloc(const void* q, int dtype, int Nq, int Hq, int Hkv,
+                                              int D, const void* k_cache, const void* v_cache,
+                                              int page_size, const int* table, int table_width,
+                                              const int* lengths, const int* ids,
+                                              const int* positions, const void* means,
+                                              int max_chunks, int chunk, int width, int R,
+                                              int dense, int* selected, void* out, float* lse,
+                                              void* stream) {
+  if (Nq < 1 || Hkv < 1 || Hq < 1 || D < 1) { moba_set_error("decode_attend_noalloc: bad sizes"); return MOBA_ERR_ARG; }
+  const int splits = uniform_splits(Nq, Hkv);
+  const int64_t rows = (int64_t)Nq * Hq * splits;
+  const int64_t part_o_bytes = (rows * D * 4 + 255) / 256 * 256;
+  const int64_t need = part_o_bytes + rows * 2 * 4;
+  if (need > (int64_t)kNoAllocScratchBytes) {
+    moba_set_error("decode_attend_noalloc: %lld bytes of split partials (Nq*Hq*splits*(D+2)*4, "
+                   "splits %d) exceed the %lld-byte static scratch; use moba_hip_decode_fused "
+                   "with caller workspaces", (long long)need, splits,
+                   (long long)kNoAllocScratchBytes);
+    return MOBA_ERR_CAPACITY;
+  }
+  void* base = nullptr;
+  if (int rc = scratch_address(&base)) return rc;
+  float* part_o = (float*)base;
+  float* part_ml = (float*)((char*)base + part_o_bytes);
+  return moba_hip_decode_fused(q, nullptr, nullptr, dtype, Nq, Hq, Hkv, D, (void*)k_cache,
+                               (void*)v_cache, page_size, (int*)table, table_width, (int*)lengths,
+                               ids, (int*)positions, nullptr, (void*)means, max_chunks, chunk,
+                               width, R, dense, 0, splits, nullptr, 0, selected, part_o, part_ml,
+                               out, lse, stream);
 }

@@ -46,6 +46,8 @@ SIGNATURES = {
     "moba_hip_decode_fused_supported": [_I, _I, _I, _I, _I],
     "moba_hip_decode_fused": [_P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _I, _P, _P, _P, _P,
                               _P, _I, _I, _I, _I, _I, _I, _I, _P, _I, _P, _P, _P, _P, _P, _P],
+    "moba_hip_decode_attend_noalloc": [_P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _I, _P, _P, _P,
+                                       _P, _I, _I, _I, _I, _I, _P, _P, _P, _P],
     # host page pool (CPU only)
     "moba_pool_create": [_I, _I, _I, _I, _I, _PP],
     "moba_pool_destroy": [_P],
@@ -86,6 +88,7 @@ class MobaHipError(RuntimeError):
 
 
 MOBA_ERR_ARG = 1
+MOBA_ERR_CAPACITY = 3
 MOBA_ERR_STALE = 4
 
 
