@@ -46,7 +46,7 @@ NO_VGPR_FORM = {"attn_dkdv.hip"}
 
 def _flags(src: Path):
     if src.suffix == ".cpp":  # host-only sources: the host compiler, HIP runtime API only
-        return ["-O2", "-std=c++17", "-fPIC", "-Wall", "-D__HIP_PLATFORM_AMD__",
+        return ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-result", "-D__HIP_PLATFORM_AMD__",
                 "-I/opt/rocm/include"]
     if src.name in NO_VGPR_FORM:
         i = FLAGS.index("-amdgpu-mfma-vgpr-form")

@@ -33,6 +33,27 @@
 
 using namespace moba;
 
+// Phase timestamps for profiling builds (-DMOBA_DECODE_TRACE): thread 0 of
+// each workgroup of fused_kernel records s_memrealtime (100 MHz) at the
+// phase boundaries below into a device array that moba_decode_trace_read
+// copies out.  Compiled out of the product library.
+#ifdef MOBA_DECODE_TRACE
+__device__ unsigned long long g_decode_trace[16 * 8192];
+extern "C" int moba_decode_trace_read(void* dst) {
+  return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_decode_trace), sizeof(g_decode_trace), 0,
+                                  hipMemcpyDeviceToHost);
+}
+#define DTRACE(i)                                                              \
+  do {                                                                         \
+    if (threadIdx.x == 0) {                                                    \
+      const unsigned wg = blockIdx.y * gridDim.x + blockIdx.x;                 \
+      if (wg < 8192) g_decode_trace[wg * 16 + (i)] = __builtin_amdgcn_s_memrealtime(); \
+    }                                                                          \
+  } while (0)
+#else
+#define DTRACE(i) do { } while (0)
+#endif
+
 namespace {
 
 constexpr int kFW = 4;          // waves per workgroup
@@ -80,7 +101,7 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
   constexpr int STAGE_BYTES = kFW * STAGE * 2;
   constexpr int MERGE_BYTES = kFW * (16 * DP + 32) * 4;
   constexpr int VLD = 32 * (DP / 8) / 64;  // 16-byte V chunks per lane per block
-  static_assert((64 * (DP + 8) + 16 * DP) * 2 <= (STAGE_BYTES > MERGE_BYTES ? STAGE_BYTES : MERGE_BYTES),
+  static_assert(64 * (DP + 8) * 2 + 16 * DP * 4 <= (STAGE_BYTES > MERGE_BYTES ? STAGE_BYTES : MERGE_BYTES),
                 "route staging must fit the V-tile / merge buffer");
   __shared__ __attribute__((aligned(16))) unsigned char lds[STAGE_BYTES > MERGE_BYTES ? STAGE_BYTES : MERGE_BYTES];
   extern __shared__ int dyn[];
@@ -97,46 +118,27 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
   const int qrow = rowk / a.Hkv, kh = rowk % a.Hkv;
   const int G = a.G, D = a.D, C = a.C, width = a.width;
 
-  if (tid == 0) {
-    const int sid = a.ids[qrow];
-    int p;
-    if (a.pos_mode == 0) {
-      p = a.positions[qrow];
-    } else {
-      const int len = a.lengths[sid];
-      p = a.pos_mode == 2 ? len : len - 1;
-    }
-    s_info[0] = sid;
-    s_info[1] = p;
-    s_info[2] = a.delta ? a.delta[qrow] : -1;
-    s_info[3] = a.delta ? a.delta[a.Nq + qrow] : -1;
-  }
-  __syncthreads();
-  const int sid = s_info[0], p = s_info[1], dl = s_info[2], dp = s_info[3];
-  const bool step = a.pos_mode == 2;
-  if (p < 0 || p / C > width) return;  // caller contract: width covers every position
+  DTRACE(0);
+  // Row state comes from uniform (scalar) loads; the loads that need only the
+  // slot (q rows, the first 64 closed-chunk means, the page-table row) are
+  // issued before the position is known, so they overlap the lengths load.
+  const int sid = a.ids[qrow];
   const int* trow = a.table + (int64_t)sid * a.W;
-  // One burst of loads, all depending only on (sid, p): the row's page-table
-  // entries up to the query's page (every page lookup below then reads LDS,
-  // so no global load waits behind the K/V stream; W <= kTblMax is a launch
-  // precondition), the group's q rows and the first 64 closed-chunk means.
   int* tbl = dyn + (G * width + 3 * (width + 1) + (width + 2) + 16 * kMaxSlots);
-  const int npg = min(p / a.P + 1, a.W);
-  const int cur = p / C;  // the current chunk (always attended, by every head)
-  const int legal = a.dense ? 0 : min(cur, width);  // chunks c with (c + 1) * C <= p
   constexpr int RC = DP / 8;                  // 16-byte pieces per row
   constexpr int NSTG = (64 * RC + 64 * kFW - 1) / (64 * kFW);
   constexpr int MS = DP + 8;                         // padded row: conflict-free 16-byte reads
-  uint16_t* ms = reinterpret_cast<uint16_t*>(lds);  // [64][MS] means rows
-  uint16_t* qs = ms + 64 * MS;                       // [16][DP] q rows
-  auto load_means = [&](int c0, u16x8_t (&stg)[NSTG]) {
-    const int nc = min(64, legal - c0);
+  uint16_t* ms = reinterpret_cast<uint16_t*>(lds);  // [64][MS] means rows (cache dtype)
+  float* qsf = reinterpret_cast<float*>(ms + 64 * MS);  // [16][DP] q rows in fp32
+  auto load_means = [&](int c0, int nc, u16x8_t (&stg)[NSTG]) {
 #pragma unroll
     for (int i = 0; i < NSTG; ++i) {
       const int x = tid + i * 64 * kFW, cl = x / RC, j = x % RC;
-      stg[i] = (cl < nc && j * 8 < D)
-                   ? ld8(a.means + (((int64_t)sid * a.max_chunks + c0 + cl) * a.Hkv + kh) * D + j * 8)
-                   : zero8();
+      // issued unconditionally at a clamped address, masked after (a guarded
+      // load costs a branch and a full wait each)
+      const int clc = min(cl, nc - 1), jc = min(j, D / 8 - 1);
+      stg[i] = ld8(a.means + (((int64_t)sid * a.max_chunks + c0 + clc) * a.Hkv + kh) * D + jc * 8);
+      if (!(cl < nc && j * 8 < D)) stg[i] = zero8();
     }
   };
   auto store_means = [&](const u16x8_t (&stg)[NSTG]) {
@@ -146,24 +148,40 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
       if (cl < 64) st8(ms + cl * MS + j * 8, stg[i]);
     }
   };
+  constexpr int NQ = (16 * RC + 64 * kFW - 1) / (64 * kFW);
+  u16x8_t qv[NQ], stg[NSTG];
+  int t[4];
   {
-    int t[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int x = tid + i * 64 * kFW;
-      t[i] = x < npg ? trow[x] : -1;
-    }
-    constexpr int NQ = (16 * RC + 64 * kFW - 1) / (64 * kFW);
-    u16x8_t qv[NQ];
 #pragma unroll
     for (int i = 0; i < NQ; ++i) {
       const int x = tid + i * 64 * kFW, qg = x / RC, qj = x % RC;
-      qv[i] = (!a.dense && qg < G && qj * 8 < D)
-                  ? ld8(a.q + ((int64_t)qrow * a.Hq + kh * G + qg) * D + qj * 8)
-                  : zero8();
+      qv[i] = ld8(a.q + ((int64_t)qrow * a.Hq + kh * G + min(qg, G - 1)) * D +
+                  min(qj, D / 8 - 1) * 8);
+      if (!(qg < G && qj * 8 < D)) qv[i] = zero8();
     }
-    u16x8_t stg[NSTG];
-    if (legal > 0) load_means(0, stg);
+    // rows past the position's closed chunks are staged but never scored
+    if (!a.dense) load_means(0, min(64, width), stg);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int x = tid + i * 64 * kFW;
+      t[i] = trow[min(x, a.W - 1)];
+    }
+  }
+  int p;
+  if (a.pos_mode == 0) {
+    p = a.positions[qrow];
+  } else {
+    const int len = a.lengths[sid];
+    p = a.pos_mode == 2 ? len : len - 1;
+  }
+  const int dl = a.delta ? a.delta[qrow] : -1, dp = a.delta ? a.delta[a.Nq + qrow] : -1;
+  DTRACE(1);
+  const bool step = a.pos_mode == 2;
+  if (p < 0 || p / C > width) return;  // caller contract: width covers every position
+  const int npg = min(p / a.P + 1, a.W);
+  const int cur = p / C;  // the current chunk (always attended, by every head)
+  const int legal = a.dense ? 0 : min(cur, width);  // chunks c with (c + 1) * C <= p
+  {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int x = tid + i * 64 * kFW;
@@ -172,19 +190,26 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
 #pragma unroll
     for (int i = 0; i < NQ; ++i) {
       const int x = tid + i * 64 * kFW, qg = x / RC, qj = x % RC;
-      if (!a.dense && qg < G) st8(qs + qg * DP + qj * 8, qv[i]);
+      if (!a.dense && qg < G) {
+        f32x4_t lo, hi;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { lo[e] = to_f32<DT>(qv[i][e]); hi[e] = to_f32<DT>(qv[i][4 + e]); }
+        *reinterpret_cast<f32x4_t*>(qsf + qg * DP + qj * 8) = lo;
+        *reinterpret_cast<f32x4_t*>(qsf + qg * DP + qj * 8 + 4) = hi;
+      }
     }
-    if (legal > 0) store_means(stg);
+    if (!a.dense) store_means(stg);
     for (int x0 = 4 * 64 * kFW; x0 < npg; x0 += 64 * kFW) {  // long rows
       const int x = x0 + tid;
       if (x < npg) tbl[x] = trow[x];
     }
   }
   __syncthreads();
+  DTRACE(2);
   // page of logical slot `slot`; the page-table delta of this launch wins
   auto page_at = [&](int slot) -> int { return slot == dl ? dp : tbl[slot]; };
 
-  // ---- side work of a step: scatter + table delta (split 0), closing mean (last split)
+  // ---- side work of a step: table delta + scatter (split 0), closing mean
   if (a.pos_mode != 0 && split == 0 && kh == 0 && tid == 0 && dl >= 0)
     a.table[(int64_t)sid * a.W + dl] = dp;
   if (step && split == 0) {
@@ -198,25 +223,32 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
       }
     }
   }
-  if (step && split == S - 1 && (p + 1) % C == 0) {
-    // canonical order: lane j sums tokens j, j+64, ... of the chunk, then the tree
+  if (step && (p + 1) % C == 0) {
+    // The mean of the chunk this token closes, canonical order: lane j sums
+    // tokens j, j+64, ... of the chunk in order, then the fixed tree.  Its
+    // D/8 items of 8 dims are spread over the row's splits and waves (item i:
+    // split i % S, wave (i / S) % 4), each item's loads issued together.
     const int cc = p / C, nd8 = D / 8;
-    for (int item = w; item < nd8; item += kFW) {
+    for (int item = split + S * w; item < nd8; item += S * kFW) {
       const int d0 = item * 8;
       float acc[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
-      for (int t = cc * C + lane; t < (cc + 1) * C; t += 64) {
-        u16x8_t x;
-        if (t == p) {
-          x = ld8(a.k + ((int64_t)qrow * a.Hkv + kh) * D + d0);
-        } else {
-          const int pg = page_at(t / a.P);
-          if (pg < 0) continue;
-          x = ld8(a.kc + (((int64_t)pg * a.P + t % a.P) * a.Hkv + kh) * D + d0);
+      for (int t0 = 0; t0 < C; t0 += 64 * 16) {
+        u16x8_t x[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int tl = t0 + lane + 64 * i, tok = tl < C ? cc * C + tl : p;
+          const uint16_t* src =
+              tok == p ? a.k + ((int64_t)qrow * a.Hkv + kh) * D + d0
+                       : a.kc + (((int64_t)max(page_at(tok / a.P), 0) * a.P + tok % a.P) * a.Hkv + kh) * D + d0;
+          x[i] = ld8(src);
+          if (tl >= C) x[i] = zero8();
         }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] = acc[e] + to_f32<DT>(x[e]);
+        for (int i = 0; i < 16; ++i)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[e] = acc[e] + to_f32<DT>(x[i][e]);
       }
       uint16_t res[8];
 #pragma unroll
@@ -228,6 +260,7 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
       }
     }
   }
+  DTRACE(3);
 
   // ---- route: scores, stable top-R per head, union of the chosen chunks
   float* sc = reinterpret_cast<float*>(dyn);
@@ -241,41 +274,49 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
   for (int c = tid; c <= cur; c += 64 * kFW) umask[c] = (a.dense || c == cur) ? all_heads : 0;
   for (int x = tid; x < G * S1; x += 64 * kFW) sel_s[x] = x % S1 == 0 ? cur : -1;
   if (!a.dense) {
-    // each score is a sequential fma chain over d against LDS-staged rows
+    // Scores: thread x takes (head x / nc, chunk x % nc) of the tile; each
+    // score is the sequential fp32 fma chain over d of the staged mean row
+    // and the head's q row (fp32 in LDS).
     for (int c0 = 0; c0 < legal; c0 += 64) {
       const int nc = min(64, legal - c0);
       if (c0 > 0) {  // the first 64 means rows came with the first burst
-        u16x8_t stg[NSTG];
-        load_means(c0, stg);
+        load_means(c0, nc, stg);
         __syncthreads();  // the previous tile's scores are done
         store_means(stg);
         __syncthreads();
       }
       for (int x = tid; x < G * nc; x += 64 * kFW) {
         const int g = x / nc, cl = x % nc;
+        const float* qg = qsf + g * DP;
+        const uint16_t* mr = ms + cl * MS;
         float acc = 0.0f;
-        // Operands of 8 pieces (64 d) are read in one batch, then the fma
-        // chain runs on registers.  Pieces past D are zero in both staged
-        // rows, and fma(0, 0, acc) == acc, so the chain runs over all DP
-        // without a branch per piece.
+        // operands of 8 pieces (64 d) are read in one batch, then the chain
+        // runs on registers; pieces past D are zero in both rows, and
+        // fma(0, 0, acc) == acc
         constexpr int JB = RC < 8 ? RC : 8;
 #pragma unroll
         for (int j0 = 0; j0 < RC; j0 += JB) {
-          u16x8_t mv[JB], qv[JB];
+          u16x8_t mv[JB];
+          f32x4_t qa[JB], qb[JB];
 #pragma unroll
           for (int j = 0; j < JB; ++j) {
-            mv[j] = ld8(ms + cl * MS + (j0 + j) * 8);
-            qv[j] = ld8(qs + g * DP + (j0 + j) * 8);
+            mv[j] = ld8(mr + (j0 + j) * 8);
+            qa[j] = *reinterpret_cast<const f32x4_t*>(qg + (j0 + j) * 8);
+            qb[j] = *reinterpret_cast<const f32x4_t*>(qg + (j0 + j) * 8 + 4);
           }
 #pragma unroll
-          for (int j = 0; j < JB; ++j)
+          for (int j = 0; j < JB; ++j) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc = fmaf(to_f32<DT>(mv[j][e]), to_f32<DT>(qv[j][e]), acc);
+            for (int e = 0; e < 4; ++e) acc = fmaf(to_f32<DT>(mv[j][e]), qa[j][e], acc);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc = fmaf(to_f32<DT>(mv[j][4 + e]), qb[j][e], acc);
+          }
         }
         sc[g * width + c0 + cl] = acc;
       }
     }
     __syncthreads();
+    DTRACE(4);
     // stable top-R by rank: chunk c of head g takes slot 1 + rank, where rank
     // counts the chunks ahead of it in (score desc, chunk asc) order; -inf
     // and NaN scores are never selected.  Same picks as R rounds of "best
@@ -317,6 +358,7 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
     }
   }
   __syncthreads();
+  DTRACE(5);
   if (!a.dense && split == 0 && a.selected != nullptr) {
     for (int x = tid; x < G * S1; x += 64 * kFW) {
       const int g = x / S1, j = x % S1;
@@ -357,6 +399,7 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
   }
   __syncthreads();
   const int n_items = s_info[4], NB = s_info[5];
+  DTRACE(6);
   const int b0 = (int)((int64_t)split * NB / S), b1 = (int)((int64_t)(split + 1) * NB / S);
 
   // ---- attention over blocks [b0, b1)
@@ -522,6 +565,7 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
 
   // ---- merge the 4 waves in LDS into this split's partial per head
   __syncthreads();  // all V tiles consumed: the merge buffer aliases them
+  DTRACE(7);
   float* mrg = reinterpret_cast<float*>(lds);
   {
     float* wo = mrg + w * (16 * DP + 32);
@@ -555,6 +599,7 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
     a.part_o[entry * D + d] = z > 0.0f ? acc / z : 0.0f;
     if (d == 0) { a.part_ml[2 * entry] = M; a.part_ml[2 * entry + 1] = z; }
   }
+  DTRACE(8);
 }
 
 // Combines the S split partials of one (query, q head): weights
