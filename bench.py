@@ -2,29 +2,39 @@
 """MoBA on one MI355X: the BASELINE.json headline workloads.
 
 Default run (N=1):
-  * headline  : cfg3, 32K MHA prefill fwd+bwd through the `opt_hip` registry
-                entry (T=32768, 32 heads, D=128, chunk 4096, topk 3, bf16,
-                Q/K/V/dO iid N(0,1)/sqrt(128)); ms per step and MFMA%
-                (algorithmic FLOPs: attended pairs x (4D fwd + 10D bwd)).
-  * roofline  : the key-major dK/dV backward kernel, timed live with stream
-                events around its launch inside every timed step; `traffic`
-                is its HBM bytes per launch from the copy-calibrated rocprofv3
-                FETCH_SIZE / WRITE_SIZE passes in profiles/dkdv_cfg3_traffic.*.
-  * gqa_16k   : cfg2 (Qwen2-0.5B GQA 14/2, D=64, T=16384, chunk 2048).
-  * decode    : cfg4, batch-8 paged decode (12q/2kv, D=128, bf16, ctx
-                U[2048,16384], page 48, chunk 512, topk 4, shuffled page pool),
-                PreparedDecode step replayed as a hipGraph; us/step and the
-                logical K/V bytes the routes require per step.
-  * decode_mqa: cfg5, batch-32 MQA fp16 graph decode (D=96, page 64, chunk
-                1024, topk 8, 256 steps).
+  * headline   : cfg3, 32K MHA prefill fwd+bwd through the `opt_hip` registry
+                 entry (T=32768, 32 heads, D=128, chunk 4096, topk 3, bf16,
+                 Q/K/V/dO iid N(0,1)/sqrt(128)); ms per step and MFMA%
+                 (algorithmic FLOPs: attended pairs x (4D fwd + 10D bwd)).
+  * gqa_16k    : cfg2 (Qwen2-0.5B GQA 14/2, D=64, T=16384, chunk 2048).
+                 cfg3 and cfg2 run in rounds of alternating order (AB / BA);
+                 each step is timed with stream events and a config's figure
+                 is the median of its per-round medians, the statistic of
+                 benchmarks/benchmark_attention.py:245-256; min / max of the
+                 round medians are reported beside it.
+  * roofline   : the key-major dK/dV backward kernel of cfg3, timed live with
+                 stream events around its launch in every timed step;
+                 `traffic` is its HBM bytes per launch from the copy-
+                 calibrated rocprofv3 FETCH_SIZE / WRITE_SIZE passes in
+                 profiles/dkdv_cfg3_traffic.*.
+  * decode     : cfg4, batch-8 paged decode (12q/2kv, D=128, bf16, ctx
+                 U[2048,16384], page 48, chunk 512, topk 4, shuffled page
+                 pools), PreparedDecode steps replayed from their hipGraph
+                 (the headline decode figure) and eager beside it.  Steps
+                 rotate over several independent caches whose pools together
+                 exceed the 256 MB Infinity Cache, so K/V come from HBM.
+                 Bytes per step are the unique K/V bytes the routes need.
+  * decode_mqa : cfg5, batch-32 MQA fp16 graph decode (D=96, page 64, chunk
+                 1024, topk 8, 256 steps), measured the same way.
   * cpu_baseline: the FP64 CPU oracle (routing + fixed-route fwd + bwd) on 1 of
-                the 32 heads of cfg3, scaled x32, on this host's cores.
+                 the 32 heads of cfg3, scaled x32, on this host's cores.
 Prints ONE JSON line on stdout; progress goes to stderr.
 """
 import argparse
 import json
 import os
 import random
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -36,86 +46,122 @@ for p in (ROOT, ROOT / "moba-merge-cuda_amd"):
 
 BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
-METRIC = BASELINE_METRIC = ("prefill fwd+bwd ms & MFMA% (32K); paged decode µs/step & "
-                            "HBM GB/s (bs 8)")
+MALL_BYTES = 256 << 20     # MI355X Infinity Cache
+METRIC = ("prefill fwd+bwd ms & MFMA% (32K); paged decode µs/step & HBM GB/s (bs 8)")
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def _spread(xs):
+    return {"median": statistics.median(xs), "min": min(xs), "max": max(xs)}
+
+
 # ------------------------------------------------------------------ prefill
 
-def prefill_inputs(T, hq, hkv, d, scale, seed, dtype):
+class PrefillCase:
+    """One prefill configuration with its inputs resident in HBM."""
+
+    def __init__(self, name, T, hq, hkv, d, chunk, topk, scale, seed):
+        import torch
+        import moba_hip  # noqa: F401
+        self.name, self.T, self.d = name, T, d
+        g = torch.Generator(device="cuda").manual_seed(seed)
+
+        def rnd(h):
+            return (torch.randn((T, h, d), generator=g, device="cuda") * scale).to(torch.bfloat16)
+        self.q, self.k, self.v, self.do = rnd(hq), rnd(hkv), rnd(hkv), rnd(hq)
+        for t in (self.q, self.k, self.v):
+            t.requires_grad_(True)
+        self.cu = torch.tensor([0, T], device="cuda", dtype=torch.int32)
+        self.cfg = {"chunk_size": chunk, "topk": topk}
+        self.shape = (hq, hkv, chunk, topk)
+
+    def step(self):
+        import torch
+        import moba_hip
+        out = moba_hip.run_impl("opt_hip", self.q, self.k, self.v, self.cu, self.T, self.cfg)
+        return torch.autograd.grad(out, (self.q, self.k, self.v), grad_outputs=self.do)
+
+    def flops(self):
+        """Algorithmic FLOPs of one fwd+bwd step: attended (q head, key)
+        pairs x 14 D; and the 8 D per pair of the key-major dK/dV kernel."""
+        from moba_hip.ops import prefill as P
+        hq, hkv, chunk, topk = self.shape
+        plan = P.get_plan([0, self.T], chunk, hq, hkv, self.d, topk, self.q.device)
+        rt = P.route(plan, self.q.detach(), self.k.detach(), 0)
+        self_pairs = sum((b - a) * (b - a + 1) // 2
+                         for a, b in zip(plan.cu_chunk[:-1], plan.cu_chunk[1:]))
+        pairs = self_pairs * hq + int(rt.counts.sum().item()) * chunk
+        return pairs, pairs * 14 * self.d, pairs * 8 * self.d
+
+
+def time_steps(case, n, dkdv=None):
+    """Runs n steps with a stream event before each and after the last;
+    returns the per-step GPU times (ms).  dkdv collects the dK/dV launch
+    times (ms) when given."""
     import torch
-    g = torch.Generator(device="cuda").manual_seed(seed)
-
-    def rnd(h):
-        return (torch.randn((T, h, d), generator=g, device="cuda") * scale).to(dtype)
-    q, k, v = rnd(hq), rnd(hkv), rnd(hkv)
-    do = rnd(hq)
-    return q, k, v, do
-
-
-def attended_pairs(plan, rt, chunk):
-    self_pairs = 0
-    for a, b in zip(plan.cu_chunk[:-1], plan.cu_chunk[1:]):
-        n = b - a
-        self_pairs += n * (n + 1) // 2
-    remote = int(rt.counts.sum().item()) * chunk
-    return self_pairs * plan.hq + remote
-
-
-def bench_prefill(T, hq, hkv, d, chunk, topk, steps, warmup, scale, seed, time_dkdv=False):
-    import torch
-    import moba_hip
     from moba_hip.ops import prefill as P
-    dtype = torch.bfloat16
-    q, k, v, do = prefill_inputs(T, hq, hkv, d, scale, seed, dtype)
-    q.requires_grad_(True)
-    k.requires_grad_(True)
-    v.requires_grad_(True)
-    cu = torch.tensor([0, T], device="cuda", dtype=torch.int32)
-    cfg = {"chunk_size": chunk, "topk": topk}
-
-    def step():
-        out = moba_hip.run_impl("opt_hip", q, k, v, cu, T, cfg)
-        return torch.autograd.grad(out, (q, k, v), grad_outputs=do)
-
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-    ev = []
-    if time_dkdv:
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for _ in range(steps)]
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    e0.record()
-    for i in range(steps):
-        if time_dkdv:
-            P.DKDV_EVENTS = ev[i]
-        step()
-    e1.record()
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) * 1e3 / steps
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+    kev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(n)] if dkdv is not None else None
+    ev[0].record()
+    for i in range(n):
+        if kev is not None:
+            P.DKDV_EVENTS = kev[i]
+        case.step()
+        ev[i + 1].record()
     P.DKDV_EVENTS = None
-    gpu_ms = e0.elapsed_time(e1) / steps
-    plan = P.get_plan([0, T], chunk, hq, hkv, d, topk, q.device)
-    rt = P.route(plan, q.detach(), k.detach(), 0)
-    pairs = attended_pairs(plan, rt, chunk)
-    flops = pairs * 14 * d
-    res = {"ms_per_step": wall, "gpu_ms_per_step": gpu_ms, "attended_pairs": pairs,
-           "algorithmic_tflop": flops / 1e12, "tflops": flops / wall / 1e9,
-           "mfma_frac": flops / wall / 1e9 / BF16_PEAK_TFLOPS}
-    if time_dkdv:
-        dk_ms = sum(a.elapsed_time(b) for a, b in ev) / steps
-        res["dkdv_ms"] = dk_ms
-        res["dkdv_tflop"] = pairs * 8 * d / 1e12
-    del q, k, v, do
+    torch.cuda.synchronize()
+    if kev is not None:
+        dkdv.extend(a.elapsed_time(b) for a, b in kev)
+    return [ev[i].elapsed_time(ev[i + 1]) for i in range(n)]
+
+
+def bench_prefill(steps, warmup, seed):
+    """cfg3 (headline) and cfg2 in rounds of alternating order; exactly
+    `steps` timed steps of each, bracketed by synchronisations."""
+    import torch
+    cases = [PrefillCase("cfg3", 32768, 32, 32, 128, 4096, 3, 128 ** -0.5, seed),
+             PrefillCase("cfg2", 16384, 14, 2, 64, 2048, 3, 1.0, seed + 1)]
+    for c in cases:
+        for _ in range(warmup):
+            c.step()
+    rounds = max(1, min(5, steps))
+    per = [steps // rounds + (1 if r < steps % rounds else 0) for r in range(rounds)]
+    res = {c.name: {"round_medians": [], "steps": [], "wall": 0.0} for c in cases}
+    dkdv = []
+    for r in range(rounds):
+        order = cases if r % 2 == 0 else cases[::-1]
+        for c in order:
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            ts = time_steps(c, per[r], dkdv if c.name == "cfg3" else None)
+            torch.cuda.synchronize()
+            res[c.name]["wall"] += time.perf_counter() - t0
+            res[c.name]["round_medians"].append(statistics.median(ts))
+            res[c.name]["steps"].extend(ts)
+    out = {}
+    for c in cases:
+        pairs, flops, kflops = c.flops()
+        rm = res[c.name]["round_medians"]
+        ms = statistics.median(rm)
+        out[c.name] = {
+            "ms_per_step": ms, "round_medians_ms": rm, "rounds": rounds,
+            "spread_ms": {"min_round": min(rm), "max_round": max(rm),
+                          "min_step": min(res[c.name]["steps"]),
+                          "max_step": max(res[c.name]["steps"])},
+            "wall_ms_per_step": res[c.name]["wall"] * 1e3 / steps,
+            "attended_pairs": pairs, "algorithmic_tflop": flops / 1e12,
+            "tflops": flops / ms / 1e9, "mfma_frac": flops / ms / 1e9 / BF16_PEAK_TFLOPS}
+        if c.name == "cfg3":
+            out[c.name]["dkdv_ms"] = statistics.median(dkdv)
+            out[c.name]["dkdv_ms_spread"] = [min(dkdv), max(dkdv)]
+            out[c.name]["dkdv_tflop"] = kflops / 1e12
+    del cases
     torch.cuda.empty_cache()
-    return res
+    return out
 
 
 # ------------------------------------------------------------------- decode
@@ -129,22 +175,23 @@ def decode_bytes(selected, positions, hq, hkv, d, chunk, elem):
     for b, pos in enumerate(positions):
         for kh in range(hkv):
             chunks = set(int(c) for c in selected[b, kh * G:(kh + 1) * G].reshape(-1) if c >= 0)
-            toks = sum(min(chunk, pos + 1 - c * chunk) for c in chunks)
-            total += toks * d * elem * 2
-        total += hkv * (pos // chunk) * d * elem            # means read by the router
+            total += sum(min(chunk, pos + 1 - c * chunk) for c in chunks) * d * elem * 2
+        total += hkv * (pos // chunk) * d * elem                # means read by the router
     nq = len(positions)
-    total += nq * hq * d * elem * 2 + nq * hq * 4            # q in, out + lse out
-    total += nq * hkv * d * elem * 2                          # appended K/V
+    total += nq * hq * d * elem * 2 + nq * hq * 4              # q in, out + lse out
+    total += nq * hkv * d * elem * 2                           # appended K/V
     return total
 
 
-def build_cache(batch, lengths, hq, hkv, d, page, chunk, dtype, extra, seed):
+def build_cache(batch, lengths, hkv, d, page, chunk, dtype, extra, seed):
+    """A cache of `lengths` tokens per sequence with a seeded, shuffled free
+    page order (a fragmented physical pool, as benchmark_prepared.py:79-81)."""
     import torch
     import moba_hip
     cache = moba_hip.PagedKVCache(batch, max(lengths) + extra, hkv, d, page_size=page,
                                   chunk_size=chunk, dtype=dtype)
     pages = list(cache._layout.free_pages)
-    random.Random(seed).shuffle(pages)   # fragmented physical pool
+    random.Random(seed).shuffle(pages)
     cache._layout.free_pages = tuple(pages)
     g = torch.Generator(device="cuda").manual_seed(seed)
     for sid, length in enumerate(lengths):
@@ -156,80 +203,106 @@ def build_cache(batch, lengths, hq, hkv, d, page, chunk, dtype, extra, seed):
     return cache
 
 
-def bench_decode(batch, hq, hkv, d, page, chunk, topk, lo, hi, steps, warmup, dtype_name, seed):
+def bench_decode(batch, hq, hkv, d, page, chunk, topk, lo, hi, steps, warmup, dtype_name, seed,
+                 rounds=4):
     import numpy as np
     import torch
     dtype = torch.bfloat16 if dtype_name == "bf16" else torch.float16
-    elem = 2
     rng = random.Random(seed)
     lengths = [rng.randint(lo, hi) for _ in range(batch)]
-    extra = 2 * (warmup + steps) + 4
     g = torch.Generator(device="cuda").manual_seed(seed + 1)
     q = torch.randn((batch, hq, d), generator=g, device="cuda", dtype=dtype)
     kn = torch.randn((batch, hkv, d), generator=g, device="cuda", dtype=dtype)
     vn = torch.randn((batch, hkv, d), generator=g, device="cuda", dtype=dtype)
+    extra = 2 * (warmup + steps) + 8
 
-    # pass 1 (untimed): record the routes of every step to count the bytes
-    cache = build_cache(batch, lengths, hq, hkv, d, page, chunk, dtype, extra, seed)
+    # pass 1 (untimed): the routes of every step of cache 0, to count bytes
+    cache = build_cache(batch, lengths, hkv, d, page, chunk, dtype, extra, seed)
+    pool_bytes = cache.k_cache.numel() * cache.k_cache.element_size() * 2
     byte_counts = []
     with cache.prepare_decode(list(range(batch)), hq, topk=topk, check_finite=False) as p:
         for i in range(warmup + steps):
             r = p.step(q, kn, vn)
             if i >= warmup:
                 byte_counts.append(decode_bytes(r.selected_blocks.cpu().numpy(), r.positions,
-                                                hq, hkv, d, chunk, elem))
-    del cache
+                                                hq, hkv, d, chunk, 2))
+    del cache, p
     torch.cuda.empty_cache()
 
-    # pass 2 (timed): identical state; eager steps, then graph-replayed steps
-    cache = build_cache(batch, lengths, hq, hkv, d, page, chunk, dtype, extra, seed)
-
-    def timed(fn, n):
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        t0 = time.perf_counter()
-        e0.record()
-        for _ in range(n):
-            fn()
-        e1.record()
-        torch.cuda.synchronize()
-        return (time.perf_counter() - t0) * 1e6 / n, e0.elapsed_time(e1) * 1e3 / n
-
-    with cache.prepare_decode(list(range(batch)), hq, topk=topk, check_finite=False) as p:
-        # the prepared workspaces are the inputs (no staging copies)
+    # pass 2 (timed): n caches rotated per step, pools together > the MALL
+    n = max(3, -(-3 * MALL_BYTES // pool_bytes))
+    caches = [build_cache(batch, lengths, hkv, d, page, chunk, dtype, extra, seed + i)
+              for i in range(n)]
+    plans = [c.prepare_decode(list(range(batch)), hq, topk=topk, check_finite=False)
+             for c in caches]
+    for p in plans:  # the bound input buffers are the inputs (no staging copies)
         p.q.copy_(q)
         p.k.copy_(kn)
         p.v.copy_(vn)
-        for _ in range(warmup):
-            p.step(p.q, p.k, p.v)
-        eager_wall, eager_gpu = timed(lambda: p.step(p.q, p.k, p.v), steps)
         p.capture("step")
-        for _ in range(warmup):
-            p.step(p.q, p.k, p.v, use_graph=True)
-        graph_wall, graph_gpu = timed(lambda: p.step(p.q, p.k, p.v, use_graph=True), steps)
-        # device time of the decode work alone: back-to-back attend launches
-        # (they read the cache and mutate nothing)
-        _, kernel_us = timed(lambda: p.attend(p.q), 50)
-        fused = p.fused
-    del cache
+    it = [0]
+
+    def run(m, graph):
+        for _ in range(m):
+            p = plans[it[0] % n]
+            p.step(p.q, p.k, p.v, use_graph=graph)
+            it[0] += 1
+
+    for graph in (False, True):
+        run(warmup, graph)
+    per = max(1, steps // rounds)
+    times = {False: [], True: []}
+    walls = {False: [], True: []}
+    for r in range(rounds):
+        for graph in ((True, False) if r % 2 == 0 else (False, True)):
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0 = time.perf_counter()
+            e0.record()
+            run(per, graph)
+            e1.record()
+            torch.cuda.synchronize()
+            walls[graph].append((time.perf_counter() - t0) * 1e6 / per)
+            times[graph].append(e0.elapsed_time(e1) * 1e3 / per)
+    fused = plans[0].fused
+    for p in plans:
+        p.close()
+    del plans, caches
     torch.cuda.empty_cache()
     mean_bytes = float(np.mean(byte_counts))
-    wall_us = min(eager_wall, graph_wall)
-    return {"us_per_step": wall_us, "eager_step_us": eager_wall, "graph_step_us": graph_wall,
-            "eager_gpu_us": eager_gpu, "graph_gpu_us": graph_gpu, "kernel_us": kernel_us,
-            "one_launch": fused,
-            "bytes_per_step": mean_bytes, "logical_gbs": mean_bytes / (wall_us * 1e-6) / 1e9,
-            "hbm_frac_logical": mean_bytes / (wall_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
-            "kernel_gbs": mean_bytes / (kernel_us * 1e-6) / 1e9,
-            "kernel_hbm_frac": mean_bytes / (kernel_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
-            "batch": batch, "contexts": lengths, "steps": steps}
+    g_us, e_us = statistics.median(walls[True]), statistics.median(walls[False])
+    return {"us_per_step": g_us, "graph_step_us": g_us, "eager_step_us": e_us,
+            "graph_round_us": walls[True], "eager_round_us": walls[False],
+            "graph_gpu_us": statistics.median(times[True]),
+            "eager_gpu_us": statistics.median(times[False]),
+            "one_launch_path": fused, "caches_rotated": n,
+            "pool_bytes_per_cache": pool_bytes,
+            "bytes_per_step": mean_bytes,
+            "graph_gbs": mean_bytes / (g_us * 1e-6) / 1e9,
+            "graph_hbm_frac": mean_bytes / (g_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+            "eager_gbs": mean_bytes / (e_us * 1e-6) / 1e9,
+            "eager_hbm_frac": mean_bytes / (e_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+            "batch": batch, "contexts": lengths, "steps": per * rounds, "rounds": rounds}
+
+
+def decode_roofline(res, name):
+    """Roofline of the decode step's dominant kernel from the committed
+    rocprofv3 summary (kernel time and HBM bytes by counter), or None."""
+    f = ROOT / "profiles" / f"decode_{name}_traffic.json"
+    if not f.exists():
+        return None
+    t = json.loads(f.read_text())
+    ach = res["bytes_per_step"] / (t["kernel_us"] * 1e-6) / 1e9
+    return {"bound": "hbm", "kernel": t["kernel"], "achieved": round(ach, 1),
+            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+            "traffic": t["traffic_bytes"], "counter_gbs": round(t["counter_gbs"], 1),
+            "source": f"profiles/decode_{name}_traffic.md"}
 
 
 # -------------------------------------------------------------- CPU baseline
 
 def cpu_baseline(seed):
     """FP64 oracle (routing + forward + backward) on head 0 of cfg3, x32."""
-    import numpy as np
     import torch
     from oracle import oracle as O
     T, d, C, K = 32768, 128, 4096, 3
@@ -259,7 +332,7 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode"], default=None)
+    ap.add_argument("--only", choices=["prefill", "decode", "cfg4", "cfg5"], default=None)
     ap.add_argument("--calib-copy", action="store_true",
                     help="first run one 1 GiB device-to-device copy (a known-size kernel that "
                          "calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -280,57 +353,60 @@ def main():
         del src, dst
         torch.cuda.empty_cache()
     out = {"metric": METRIC}
-    res3 = None
+    pre = None
     if args.only in (None, "prefill"):
-        log("prefill cfg3 (32K MHA fwd+bwd) ...")
-        res3 = bench_prefill(32768, 32, 32, 128, 4096, 3, args.steps, args.warmup,
-                             128 ** -0.5, args.seed, time_dkdv=True)
-        log(json.dumps(res3))
-        log("prefill cfg2 (16K GQA fwd+bwd) ...")
-        res2 = bench_prefill(16384, 14, 2, 64, 2048, 3, args.steps, args.warmup, 1.0,
-                             args.seed + 1)
-        log(json.dumps(res2))
+        log("prefill cfg3 + cfg2 (rounds of alternating order) ...")
+        pre = bench_prefill(args.steps, args.warmup, args.seed)
+        log(json.dumps(pre))
     dec4 = dec5 = None
-    if not args.no_decode and args.only in (None, "decode"):
-        log("decode cfg4 (batch 8 paged, graph) ...")
+    if not args.no_decode and args.only in (None, "decode", "cfg4"):
+        log("decode cfg4 (batch 8 paged, graph + eager) ...")
         dec4 = bench_decode(8, 12, 2, 128, 48, 512, 4, 2048, 16384, 128, 8, "bf16", args.seed)
         log(json.dumps({k: v for k, v in dec4.items() if k != "contexts"}))
-        log("decode cfg5 (batch 32 MQA fp16, graph) ...")
+    if not args.no_decode and args.only in (None, "decode", "cfg5"):
+        log("decode cfg5 (batch 32 MQA fp16, graph + eager) ...")
         dec5 = bench_decode(32, 16, 1, 96, 64, 1024, 8, 1024, 32768, 256, 8, "fp16",
                             args.seed + 2)
         log(json.dumps({k: v for k, v in dec5.items() if k != "contexts"}))
 
-    if res3 is not None:
-        ach = res3["dkdv_tflop"] / (res3["dkdv_ms"] * 1e-3)
+    if pre is not None:
+        r3 = pre["cfg3"]
+        ach = r3["dkdv_tflop"] / (r3["dkdv_ms"] * 1e-3)
         traffic = None
         tfile = ROOT / "profiles" / "dkdv_cfg3_traffic.json"
         if tfile.exists():  # rocprofv3 FETCH_SIZE + WRITE_SIZE passes, copy-calibrated
             traffic = json.loads(tfile.read_text())["traffic_bytes"]
         out.update({
-            "value": round(res3["ms_per_step"], 3), "unit": "ms per 32K MHA prefill fwd+bwd step",
+            "value": round(r3["ms_per_step"], 3), "unit": "ms per 32K MHA prefill fwd+bwd step",
             "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-            "ms_per_step": round(res3["ms_per_step"], 3), "higher_is_better": False,
+            "ms_per_step": round(r3["wall_ms_per_step"], 3), "higher_is_better": False,
             "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
             "data": "synthetic (seeded iid N(0,1) Q/K/V/dO, scaled 1/sqrt(128))",
             "config": {"workload": "cfg3: MoBA MHA prefill fwd+bwd, T=32768, heads=32, D=128, "
                                    "chunk=4096, topk=3, causal, bf16",
                        "entry": "moba_hip.run_impl('opt_hip')", "seq_len": 32768},
-            "mfma_frac": round(res3["mfma_frac"], 4),
-            "tflops": round(res3["tflops"], 1),
+            "statistic": "value: median of per-round medians of per-step stream-event times "
+                         "(rounds alternate cfg3/cfg2 order); ms_per_step: wall clock of the "
+                         "timed steps / steps",
+            "mfma_frac": round(r3["mfma_frac"], 4),
+            "tflops": round(r3["tflops"], 1),
             "roofline": {"bound": "mfma", "kernel": "dkdv2_kernel<bf16,128>",
                          "achieved": round(ach, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(ach / BF16_PEAK_TFLOPS, 4), "traffic": traffic,
                          "traffic_unit": "bytes per launch (profiles/dkdv_cfg3_traffic.md)",
-                         "avg_launch_ms": round(res3["dkdv_ms"], 3),
-                         "algorithmic_tflop_per_launch": round(res3["dkdv_tflop"], 3)},
-            "prefill_32k": res3, "gqa_16k": res2,
+                         "avg_launch_ms": round(r3["dkdv_ms"], 3),
+                         "algorithmic_tflop_per_launch": round(r3["dkdv_tflop"], 3)},
+            "prefill_32k": r3, "gqa_16k": pre["cfg2"],
         })
     else:
         out.update({"value": None, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup})
     if dec4 is not None:
+        dec4["roofline"] = decode_roofline(dec4, "cfg4")
         out["decode"] = dec4
+    if dec5 is not None:
+        dec5["roofline"] = decode_roofline(dec5, "cfg5")
         out["decode_mqa"] = dec5
-    if not args.no_cpu and res3 is not None:
+    if not args.no_cpu and pre is not None:
         log("cpu baseline (FP64 oracle, 1 of 32 heads) ...")
         out["cpu_baseline"] = cpu_baseline(args.seed)
     print(json.dumps(out), flush=True)
