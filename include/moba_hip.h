@@ -144,6 +144,30 @@ int moba_hip_prefill_bwd(const void* q, const void* k, const void* v, const void
  * moba_hip_pack_experts_work. */
 int64_t moba_hip_prefill_bwd_work(int n_kv_tiles, int kv_splits, int D);
 
+/* Standalone global-softmax merge of caller-owned partials.
+ * Replaces merge_forward(self_out, self_lse, remote_out, remote_lse, mapping,
+ * kmax, check_capacity, deterministic) (src/moba_opt/ops/bindings.cpp:6-22,
+ * src/moba_opt/ops/merge.cu:187-288).  self_out [T,H,D] and remote_out [M,D]
+ * in dtype (0 bf16, 1 fp16, 2 fp32), self_lse [T,H] and remote_lse [M] fp32
+ * natural log, mapping [M] int64 (row p = t*H + h of each remote partial).
+ * out [T,H,D] (dtype) and lse [T,H] fp32: m = max of the row's LSEs,
+ * O = (w_self o_self + sum w_j o_j) / z, z = sum w_j + w_self, L = m + log z.
+ * Always deterministic and atomic-free: remote partials are taken in
+ * ascending j (a stable radix sort by row), merged one wave64 per row.
+ * D a multiple of 8 in [8,256], kmax in [1,8].  work: moba_hip_merge_work(T*H,
+ * M) bytes.  status [2] int32 (device), written on the stream: status[0] = 1
+ * if a mapping entry lies outside [0,T*H) (ignored), status[1] = 1 if a row
+ * has more than kmax remote partials (the first kmax are used); the
+ * reference's check_capacity is the caller reading them after the call. */
+int moba_hip_merge(const void* self_out, const float* self_lse, const void* remote_out,
+                   const float* remote_lse, const int64_t* mapping, int dtype, int64_t T, int H,
+                   int D, int64_t M, int kmax, void* work, int* status, void* out, float* lse,
+                   void* stream);
+
+/* Bytes of the work buffer of moba_hip_merge for P = T*H rows and M remote
+ * partials (-1 for bad sizes).  Shape query; no reference counterpart. */
+int64_t moba_hip_merge_work(int64_t P, int64_t M);
+
 /* ----------------------------------------------------------------- decode */
 
 /* Number of work-list entries decode_route emits per (query, kv head, block

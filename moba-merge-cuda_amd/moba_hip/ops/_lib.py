@@ -33,6 +33,8 @@ SIGNATURES = {
     "moba_hip_prefill_bwd": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _I, _P, _I,
                              _P, _I, _P, _I, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _I, _P,
                              _P, _P],
+    "moba_hip_merge": [_P, _P, _P, _P, _P, _I, _L, _I, _I, _L, _I, _P, _P, _P, _P, _P],
+    "moba_hip_merge_work": [_L, _L],
     "moba_hip_decode_work_items": [_I, _I, _I],
     "moba_hip_paged_append": [_P, _P, _I, _I, _I, _I, _P, _P, _I, _P, _I, _P, _P, _P],
     "moba_hip_block_means": [_P, _I, _I, _I, _I, _P, _I, _P, _P, _I, _I, _I, _P, _I, _P],
@@ -74,7 +76,7 @@ SIGNATURES = {
     "moba_prep_schedule": [_P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P],
 }
 _I32P = ctypes.POINTER(ctypes.c_int32)
-_RESTYPES = {"moba_pool_destroy": None, "moba_prep_destroy": None,
+_RESTYPES = {"moba_hip_merge_work": ctypes.c_int64, "moba_pool_destroy": None, "moba_prep_destroy": None,
              "moba_prep_delta_uploads": ctypes.c_int64, "moba_pool_table": _I32P, "moba_pool_lengths": _I32P,
              "moba_pool_free": _I32P, "moba_hip_last_error": ctypes.c_char_p, "moba_hip_pack_experts_work": ctypes.c_int64,
              "moba_hip_prefill_bwd_work": ctypes.c_int64}

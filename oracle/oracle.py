@@ -165,6 +165,10 @@ def merge(self_out, self_lse, remote_out, remote_lse, mapping):
     ro = np.ascontiguousarray(remote_out, dtype=np.float64).reshape(-1, d)
     rl = np.ascontiguousarray(remote_lse, dtype=np.float64).reshape(-1)
     mp = np.ascontiguousarray(mapping, dtype=np.int64).reshape(-1)
+    # the C loop indexes rows by mapping: shapes and range are checked here
+    if sl.size != P or rl.size != mp.size or ro.shape[0] != mp.size or \
+            (mp.size and (mp.min() < 0 or mp.max() >= P)):
+        raise ValueError("oracle merge: inconsistent shapes or mapping out of range")
     out = np.zeros((P, d), dtype=np.float64)
     lse = np.zeros(P, dtype=np.float64)
     lib().oracle_merge(_p(so), _p(sl), P, d, _p(ro), _p(rl), _p(mp), mp.size, _p(out), _p(lse))
