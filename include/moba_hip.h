@@ -403,6 +403,15 @@ void moba_prep_destroy(void* handle);
  * on `stream`; positions[rows] receives each row's position.  use_graph
  * replays the graph of moba_prep_capture.  Input errors change nothing. */
 int moba_prep_run(void* handle, int append, int use_graph, void* stream, int32_t* positions);
+/* The three parts of moba_prep_run, for callers that put the launches of
+ * several layers into one stream sequence or one captured graph (a model
+ * decode step):  plan stages this call's page-table delta and schedule on
+ * `stream` and fills positions (host work; never inside a capture);
+ * launch enqueues the device work (capturable when use_graph is 0); commit
+ * installs the planned token in the lease (after the launches). */
+int moba_prep_plan(void* handle, int append, void* stream, int32_t* positions);
+int moba_prep_launch(void* handle, int append, int use_graph, void* stream);
+int moba_prep_commit(void* handle);
 /* Captures the launches of a step / attend into a hipGraph (nothing runs;
  * no state changes). */
 int moba_prep_capture(void* handle, int append, void* stream);

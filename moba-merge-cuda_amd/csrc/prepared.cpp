@@ -48,6 +48,8 @@ struct Prepared {
   bool sched_used = false;
   int ring_next = 0;
   int64_t delta_uploads = 0;
+  bool pending = false;            // a planned step awaiting moba_prep_commit
+  int64_t pending_version = 0;
   std::vector<int32_t> delta;      // [2 * rows] of the current plan
   std::vector<int32_t> sched_pos;  // positions of the last schedule (empty: none)
   std::vector<int32_t> sched_splits;
@@ -267,21 +269,16 @@ extern "C" int64_t moba_prep_delta_uploads(const void* h) {
   return h ? static_cast<const Prepared*>(h)->delta_uploads : -1;
 }
 
-extern "C" int moba_prep_run(void* h, int append, int use_graph, void* stream,
-                             int32_t* positions) {
+extern "C" int moba_prep_plan(void* h, int append, void* stream, int32_t* positions) {
   Prepared* p = static_cast<Prepared*>(h);
-  if (!p) return fail(MOBA_ERR_ARG, "prep_run: null handle");
+  if (!p) return fail(MOBA_ERR_ARG, "prep_plan: null handle");
   const MobaPrepDesc& d = p->d;
   hipStream_t st = (hipStream_t)stream;
-  hipGraphExec_t g = p->graph[append ? 1 : 0];
-  if (use_graph && !g)
-    return fail(MOBA_ERR_ARG, append ? "capture('step') first" : "capture('attend') first");
-  int64_t version = 0;
-  int grants = 0;
-  int rc;
+  int grants = 0, rc;
+  p->pending = false;
   if (append) {
     rc = moba_pool_plan_step(d.lease, p->ids.data(), d.rows, positions, p->delta.data(), &grants,
-                             &version);
+                             &p->pending_version);
     if (rc) return rc;
   } else {
     const int32_t* len = moba_pool_lengths(d.lease);
@@ -299,14 +296,44 @@ extern "C" int moba_prep_run(void* h, int append, int use_graph, void* stream,
     ++p->delta_uploads;
   }
   if ((rc = refresh_schedule(*p, positions, st))) return rc;
+  p->pending = append != 0;
+  return MOBA_OK;
+}
+
+extern "C" int moba_prep_launch(void* h, int append, int use_graph, void* stream) {
+  Prepared* p = static_cast<Prepared*>(h);
+  if (!p) return fail(MOBA_ERR_ARG, "prep_launch: null handle");
+  hipStream_t st = (hipStream_t)stream;
   if (use_graph) {
+    hipGraphExec_t g = p->graph[append ? 1 : 0];
+    if (!g) return fail(MOBA_ERR_ARG, append ? "capture('step') first" : "capture('attend') first");
     hipError_t e = hipGraphLaunch(g, st);
     if (e != hipSuccess) return hip_fail("prepared decode: graph launch", e);
-  } else if ((rc = launch(*p, append != 0, st))) {
-    return rc;
+    return MOBA_OK;
   }
-  if (append) return moba_pool_commit_step(d.lease, p->ids.data(), d.rows, p->delta.data(), version);
-  return MOBA_OK;
+  return launch(*p, append != 0, st);
+}
+
+extern "C" int moba_prep_commit(void* h) {
+  Prepared* p = static_cast<Prepared*>(h);
+  if (!p) return fail(MOBA_ERR_ARG, "prep_commit: null handle");
+  if (!p->pending) return MOBA_OK;
+  p->pending = false;
+  return moba_pool_commit_step(p->d.lease, p->ids.data(), p->d.rows, p->delta.data(),
+                               p->pending_version);
+}
+
+extern "C" int moba_prep_run(void* h, int append, int use_graph, void* stream,
+                             int32_t* positions) {
+  Prepared* p = static_cast<Prepared*>(h);
+  if (!p) return fail(MOBA_ERR_ARG, "prep_run: null handle");
+  if (use_graph && !p->graph[append ? 1 : 0])
+    return fail(MOBA_ERR_ARG, append ? "capture('step') first" : "capture('attend') first");
+  int rc = moba_prep_plan(h, append, stream, positions);
+  if (rc == MOBA_OK) rc = moba_prep_launch(h, append, use_graph, stream);
+  if (rc == MOBA_OK) rc = moba_prep_commit(h);
+  else p->pending = false;
+  return rc;
 }
 
 extern "C" int moba_prep_capture(void* h, int append, void* stream) {

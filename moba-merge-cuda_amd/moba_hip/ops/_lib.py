@@ -71,6 +71,9 @@ SIGNATURES = {
     "moba_prep_destroy": [_P],
     "moba_prep_run": [_P, _I, _I, _P, _P],
     "moba_prep_capture": [_P, _I, _P],
+    "moba_prep_plan": [_P, _I, _P, _P],
+    "moba_prep_launch": [_P, _I, _I, _P],
+    "moba_prep_commit": [_P],
     "moba_prep_delta_uploads": [_P],
     "moba_prep_sched_workgroups": [_I, _I, _I, _I],
     "moba_prep_schedule": [_P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P],

@@ -203,6 +203,32 @@ class PreparedDecode:
         self.failed = True
         raise _lib.MobaHipError(msg)
 
+    # parts of a step for a caller that sequences several layers' launches
+    # on one stream or in one captured graph (moba_hip.qwen2): plan (host
+    # work, before the launches), launch (device work, capturable), commit
+    def _plan_step(self, stream):
+        lib = _lib.load()
+        rc = lib.moba_prep_plan(self._handle, 1, stream, self._positions.ctypes.data)
+        if rc:
+            msg = lib.moba_hip_last_error().decode(errors="replace")
+            if rc == _lib.MOBA_ERR_ARG:
+                raise ValueError(msg)
+            self.failed = True
+            raise _lib.MobaHipError(msg)
+        return tuple(self._positions.tolist())
+
+    def _launch_step(self, stream):
+        lib = _lib.load()
+        if lib.moba_prep_launch(self._handle, 1, 0, stream):
+            self.failed = True
+            raise _lib.MobaHipError(lib.moba_hip_last_error().decode(errors="replace"))
+
+    def _commit_step(self):
+        lib = _lib.load()
+        if lib.moba_prep_commit(self._handle):
+            self.failed = True
+            raise _lib.MobaHipError(lib.moba_hip_last_error().decode(errors="replace"))
+
     def _result(self, positions):
         return DecodeResult(self.output, self.lse, None if self.dense else self.selected,
                             self.ids, positions)
