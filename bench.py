@@ -26,6 +26,9 @@ Default run (N=1):
                  Bytes per step are the unique K/V bytes the routes need.
   * decode_mqa : cfg5, batch-32 MQA fp16 graph decode (D=96, page 64, chunk
                  1024, topk 8, 256 steps), measured the same way.
+  * qwen2_decode: a randomly initialised Qwen2-1.5B-shaped model (cfg4's
+                 attention shape) decoding after an 8K MoBA prefill, per-token
+                 time eager and as one whole-model hipGraph.
   * cpu_baseline: the FP64 CPU oracle (routing + fixed-route fwd + bwd) on 1 of
                  the 32 heads of cfg3, scaled x32, on this host's cores.
 Prints ONE JSON line on stdout; progress goes to stderr.
@@ -253,6 +256,7 @@ def bench_decode(batch, hq, hkv, d, page, chunk, topk, lo, hi, steps, warmup, dt
     per = max(1, steps // rounds)
     times = {False: [], True: []}
     walls = {False: [], True: []}
+    host = {False: [], True: []}   # host time to issue the steps (before the sync)
     for r in range(rounds):
         for graph in ((True, False) if r % 2 == 0 else (False, True)):
             torch.cuda.synchronize()
@@ -261,8 +265,10 @@ def bench_decode(batch, hq, hkv, d, page, chunk, topk, lo, hi, steps, warmup, dt
             e0.record()
             run(per, graph)
             e1.record()
+            t1 = time.perf_counter()
             torch.cuda.synchronize()
             walls[graph].append((time.perf_counter() - t0) * 1e6 / per)
+            host[graph].append((t1 - t0) * 1e6 / per)
             times[graph].append(e0.elapsed_time(e1) * 1e3 / per)
     fused = plans[0].fused
     for p in plans:
@@ -274,6 +280,8 @@ def bench_decode(batch, hq, hkv, d, page, chunk, topk, lo, hi, steps, warmup, dt
     return {"us_per_step": g_us, "graph_step_us": g_us, "eager_step_us": e_us,
             "graph_round_us": walls[True], "eager_round_us": walls[False],
             "graph_gpu_us": statistics.median(times[True]),
+            "graph_host_us": statistics.median(host[True]),
+            "eager_host_us": statistics.median(host[False]),
             "eager_gpu_us": statistics.median(times[False]),
             "one_launch_path": fused, "caches_rotated": n,
             "pool_bytes_per_cache": pool_bytes,
@@ -283,6 +291,48 @@ def bench_decode(batch, hq, hkv, d, page, chunk, topk, lo, hi, steps, warmup, dt
             "eager_gbs": mean_bytes / (e_us * 1e-6) / 1e9,
             "eager_hbm_frac": mean_bytes / (e_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
             "batch": batch, "contexts": lengths, "steps": per * rounds, "rounds": rounds}
+
+
+def bench_qwen2(ctx, steps, seed):
+    """Whole-model decode of a randomly initialised Qwen2-1.5B-shaped model
+    (28 layers, hidden 1536, 12 q / 2 kv heads, head_dim 128 -- the shape of
+    cfg4), batch 1: MoBA prefill of `ctx` prompt tokens, then `steps` decode
+    tokens, eager and as one whole-model hipGraph per token."""
+    import torch
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+    from moba_hip.qwen2 import Qwen2Session
+    torch.manual_seed(seed)
+    cfg = Qwen2Config(vocab_size=151936, hidden_size=1536, intermediate_size=8960,
+                      num_hidden_layers=28, num_attention_heads=12, num_key_value_heads=2,
+                      max_position_embeddings=32768, attn_implementation="eager")
+    with torch.device("cuda"):
+        model = Qwen2ForCausalLM(cfg).to(torch.bfloat16).eval()
+    for p in model.parameters():
+        p.requires_grad_(False)
+    ids = torch.randint(0, cfg.vocab_size, (1, ctx), device="cuda")
+    toks = torch.randint(0, cfg.vocab_size, (steps + 4,)).tolist()
+    res = {"model": "Qwen2-1.5B shape, random init, bf16", "context": ctx, "steps": steps,
+           "chunk": 512, "topk": 4}
+    for backend in ("eager", "model_graph"):
+        with Qwen2Session(model, ctx + steps + 8, mode="moba", chunk=512, topk=4, page=48,
+                          backend=backend) as s:
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            s.prefill(ids)
+            torch.cuda.synchronize()
+            res["prefill_ms"] = (time.perf_counter() - t0) * 1e3
+            s.prepare()
+            for t in toks[:4]:
+                s.step(t)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for t in toks[4:]:
+                s.step(t)
+            torch.cuda.synchronize()
+            res[f"{backend}_ms_per_token"] = (time.perf_counter() - t0) * 1e3 / steps
+    del model
+    torch.cuda.empty_cache()
+    return res
 
 
 def decode_roofline(res, name):
@@ -332,7 +382,8 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode", "cfg4", "cfg5"], default=None)
+    ap.add_argument("--only", choices=["prefill", "decode", "cfg4", "cfg5", "qwen2"],
+                    default=None)
     ap.add_argument("--calib-copy", action="store_true",
                     help="first run one 1 GiB device-to-device copy (a known-size kernel that "
                          "calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -368,6 +419,12 @@ def main():
         dec5 = bench_decode(32, 16, 1, 96, 64, 1024, 8, 1024, 32768, 256, 8, "fp16",
                             args.seed + 2)
         log(json.dumps({k: v for k, v in dec5.items() if k != "contexts"}))
+
+    qw = None
+    if not args.no_decode and args.only in (None, "qwen2"):
+        log("qwen2-1.5B-shaped whole-model decode (eager and model graph) ...")
+        qw = bench_qwen2(8192, 32, args.seed)
+        log(json.dumps(qw))
 
     if pre is not None:
         r3 = pre["cfg3"]
@@ -406,6 +463,8 @@ def main():
     if dec5 is not None:
         dec5["roofline"] = decode_roofline(dec5, "cfg5")
         out["decode_mqa"] = dec5
+    if qw is not None:
+        out["qwen2_decode"] = qw
     if not args.no_cpu and pre is not None:
         log("cpu baseline (FP64 oracle, 1 of 32 heads) ...")
         out["cpu_baseline"] = cpu_baseline(args.seed)
