@@ -50,6 +50,12 @@ class _Desc(ctypes.Structure):
                     "item_counts", "part_o", "part_ml", "out", "lse", "sched")])
 
 
+def _raw_stream(index):
+    """The current stream's handle on device `index` (the raw query torch's
+    own stream object wraps)."""
+    return torch._C._cuda_getCurrentRawStream(index)
+
+
 class _SlotPartials:
     """Per-slot partials of the multi-kernel path (no split schedule)."""
     splits, sched, n_sched = 1, None, 0
@@ -74,6 +80,7 @@ class PreparedDecode:
             self.dense = contract.decode_mode(mode, topk)
             self.check_finite, self.stable_routes = check_finite, stable_routes
             self.cache = cache
+            self._dev = cache.device.index
             self._lease = IncrementalLayout(cache._layout,
                                             contract.int_vector(sequence_ids, "sequence_ids"))
             self.ids = self._lease.ids
@@ -163,7 +170,7 @@ class PreparedDecode:
                    "prepared decode is closed or no longer owns cache")])
         if self.failed:
             raise RuntimeError("CUDA execution failed; discard prepared decode and cache")
-        stream = torch.cuda.current_stream(c.device).cuda_stream
+        stream = _raw_stream(self._dev)
         _require([
             (lambda: not torch.cuda.is_current_stream_capturing(),
              "use capture(), not external capture"),
@@ -253,12 +260,15 @@ class PreparedDecode:
                       if self._bind(t, b, n)]
             if use_graph and "step" not in self._captured:
                 raise ValueError("capture('step') first")
-            positions = self._lease.positions()
-            _require([(lambda: int(positions.max()) < self._lease.max_seq_len,
-                       "append exceeds max_seq_len")])
+            positions = self._plan_step(stream)  # refuses (ValueError) before any change
             for given, buffer in copies:
                 buffer.copy_(given)
-            return self._result(self._run(True, use_graph, stream))
+            lib = _lib.load()
+            if lib.moba_prep_launch(self._handle, 1, int(use_graph), stream) or \
+                    lib.moba_prep_commit(self._handle):
+                self.failed = True
+                raise _lib.MobaHipError(lib.moba_hip_last_error().decode(errors="replace"))
+            return self._result(positions)
 
     def capture(self, kind="step"):
         """Records the device work of one step / attend into a hipGraph.
