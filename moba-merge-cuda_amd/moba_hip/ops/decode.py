@@ -68,21 +68,6 @@ def attention(q, kc, vc, table, lengths, q_seq, q_pos, work, out, lse, chunk, de
               out.data_ptr(), lse.data_ptr(), _lib.stream_of(q.device))
 
 
-def metadata(table, lengths, ids, positions, delta, append):
-    _lib.call("moba_hip_decode_metadata", table.data_ptr(), table.shape[1], lengths.data_ptr(),
-              ids.data_ptr(), positions.data_ptr(), delta.data_ptr(), ids.numel(),
-              1 if append else 0, _lib.stream_of(table.device))
-
-
-def step(table, lengths, ids, positions, delta, k, v, kc, vc, chunk, means):
-    """Fused prepared-decode prologue (metadata + append + closing-chunk mean)."""
-    b, hk, d = k.shape
-    _lib.call("moba_hip_decode_step", table.data_ptr(), table.shape[1], lengths.data_ptr(),
-              ids.data_ptr(), positions.data_ptr(), delta.data_ptr(), b, k.data_ptr(),
-              v.data_ptr(), DTYPE_CODE[k.dtype], kc.data_ptr(), vc.data_ptr(), kc.shape[1], hk, d,
-              chunk, means.data_ptr(), means.shape[1], _lib.stream_of(k.device))
-
-
 def fused_supported(hq, hkv, d, width, table_width) -> bool:
     return bool(_lib.load().moba_hip_decode_fused_supported(hq, hkv, d, width, table_width))
 
