@@ -99,7 +99,8 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
   constexpr int VS = DP + 8;
   constexpr int STAGE = 32 * VS;  // per-wave V tile (elements)
   constexpr int STAGE_BYTES = kFW * STAGE * 2;
-  constexpr int MERGE_BYTES = kFW * (16 * DP + 32) * 4;
+  constexpr int WS = DP + 4;  // merge row stride (floats): float4 stores of 16 lanes hit 16 distinct bank groups
+  constexpr int MERGE_BYTES = kFW * (16 * WS + 32) * 4;
   constexpr int VLD = 32 * (DP / 8) / 64;  // 16-byte V chunks per lane per block
   static_assert(64 * (DP + 8) * 2 + 16 * DP * 4 <= (STAGE_BYTES > MERGE_BYTES ? STAGE_BYTES : MERGE_BYTES),
                 "route staging must fit the V-tile / merge buffer");
@@ -568,35 +569,44 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
   DTRACE(7);
   float* mrg = reinterpret_cast<float*>(lds);
   {
-    float* wo = mrg + w * (16 * DP + 32);
+    float* wo = mrg + w * (16 * WS + 32);
+    // head c16's row, dims db*16 + 4*g4 .. +3: one 16-byte store per block
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) wo[c16 * DP + db * 16 + 4 * g4 + e] = oacc[db][e];
-    if (g4 == 0) { wo[16 * DP + c16] = m_run; wo[16 * DP + 16 + c16] = lsum; }
+      *reinterpret_cast<f32x4_t*>(wo + c16 * WS + db * 16 + 4 * g4) = oacc[db];
+    if (g4 == 0) { wo[16 * WS + c16] = m_run; wo[16 * WS + 16 + c16] = lsum; }
   }
   __syncthreads();
-  for (int x = tid; x < G * D; x += 64 * kFW) {
-    const int g = x / D, d = x % D;
+  // thread x: head x / (D/4), dims 4 (x % (D/4)) .. +3 (16-byte LDS reads
+  // and global stores; D is a multiple of 8)
+  const int nd4 = D / 4;
+  for (int x = tid; x < G * nd4; x += 64 * kFW) {
+    const int g = x / nd4, d = (x % nd4) * 4;
+    float mw[kFW], lw[kFW];
+#pragma unroll
+    for (int ww = 0; ww < kFW; ++ww) {
+      const float* o = mrg + ww * (16 * WS + 32);
+      mw[ww] = o[16 * WS + g];
+      lw[ww] = o[16 * WS + 16 + g];
+    }
     float M = -INFINITY;
 #pragma unroll
-    for (int ww = 0; ww < kFW; ++ww) {
-      const float* o = mrg + ww * (16 * DP + 32);
-      if (o[16 * DP + 16 + g] > 0.0f) M = fmaxf(M, o[16 * DP + g]);
-    }
-    float z = 0.0f, acc = 0.0f;
+    for (int ww = 0; ww < kFW; ++ww) M = lw[ww] > 0.0f ? fmaxf(M, mw[ww]) : M;
+    float z = 0.0f;
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ww = 0; ww < kFW; ++ww) {
-      const float* o = mrg + ww * (16 * DP + 32);
-      const float l = o[16 * DP + 16 + g];
-      if (l > 0.0f) {
-        const float f = fast_exp2(o[16 * DP + g] - M);
-        z += l * f;
-        acc += o[g * DP + d] * f;
-      }
+      const f32x4_t ov = *reinterpret_cast<const f32x4_t*>(mrg + ww * (16 * WS + 32) + g * WS + d);
+      const float f = lw[ww] > 0.0f ? fast_exp2(mw[ww] - M) : 0.0f;
+      z += lw[ww] * f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] += lw[ww] > 0.0f ? ov[e] * f : 0.0f;
     }
+    const float iz = z > 0.0f ? 1.0f / z : 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] *= iz;
     const int64_t entry = ((int64_t)qrow * a.Hq + kh * G + g) * a.smax + split;
-    a.part_o[entry * D + d] = z > 0.0f ? acc / z : 0.0f;
+    *reinterpret_cast<f32x4_t*>(a.part_o + entry * D + d) = acc;
     if (d == 0) { a.part_ml[2 * entry] = M; a.part_ml[2 * entry + 1] = z; }
   }
   DTRACE(8);
