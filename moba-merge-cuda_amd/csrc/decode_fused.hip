@@ -178,6 +178,9 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
   const int dl = a.delta ? a.delta[qrow] : -1, dp = a.delta ? a.delta[a.Nq + qrow] : -1;
   DTRACE(1);
   const bool step = a.pos_mode == 2;
+  // the position is published for the merge launch before any early exit (no
+  // workgroup of this launch reads it in prepared modes)
+  if (a.pos_mode != 0 && split == 0 && kh == 0 && tid == 0) a.positions[qrow] = p;
   if (p < 0 || p / C > width) return;  // caller contract: width covers every position
   const int npg = min(p / a.P + 1, a.W);
   const int cur = p / C;  // the current chunk (always attended, by every head)
@@ -617,9 +620,10 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
 // (natural log on output).  Wave w takes splits w, w + 4, ...: every partial
 // load is issued before any arithmetic.
 // Each wave sums its splits in order, then the 4 wave sums are added in wave
-// order (deterministic for a fixed S).  In prepared modes head 0 also
-// publishes the row's position (and, in step mode, advances its length):
-// every attention workgroup has read it by now.
+// order (deterministic for a fixed S).  The row's position is read from
+// `positions` (given in mode 0, published by the attention launch
+// otherwise); in step mode head 0 advances the row's length: every attention
+// workgroup has read it by now.
 constexpr int kMergeWaves = 4;
 constexpr int kMergePer = 64 / kMergeWaves;  // splits per wave (S <= 64)
 
@@ -631,14 +635,9 @@ __global__ __launch_bounds__(64 * kMergeWaves) void merge_kernel(FusedArgs a) {
   // the row's position decides only whether anything is written: its loads
   // (ids -> lengths) run beside the partial loads below, which stay inside
   // the row's own slots either way
-  const int sid = a.ids[qrow];
-  int p;
-  if (a.pos_mode == 0) {
-    p = a.positions[qrow];
-  } else {
-    const int len = a.lengths[sid];
-    p = a.pos_mode == 2 ? len : len - 1;
-  }
+  // the row's position: given (mode 0) or published by the attention launch
+  // (one load; the slot id is needed only for the length store at the end)
+  const int p = a.positions[qrow];
   const int64_t e0 = (int64_t)rh * a.smax;
   const int d = lane * 4;
   const bool dok = d < a.D;
@@ -706,10 +705,7 @@ __global__ __launch_bounds__(64 * kMergeWaves) void merge_kernel(FusedArgs a) {
   }
   if (lane == 0) {
     a.lse[rh] = (M + log2f(Z)) * kLn2;
-    if (a.pos_mode != 0 && h == 0) {
-      a.positions[qrow] = p;
-      if (a.pos_mode == 2) a.lengths[sid] = p + 1;
-    }
+    if (a.pos_mode == 2 && h == 0) a.lengths[a.ids[qrow]] = p + 1;
   }
 }
 
