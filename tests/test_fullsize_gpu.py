@@ -175,3 +175,45 @@ def test_decode_full_size(cuda_device, batch, hq, hkv, d, page, chunk, topk, lo,
             kn = torch.randn((batch, hkv, d), generator=g, device="cuda").to(dtype)
             vn = torch.randn((batch, hkv, d), generator=g, device="cuda").to(dtype)
             check(cache, plan.step(q, kn, vn), q)
+
+
+@pytest.mark.parametrize("batch,hq,hkv,d,page,chunk,topk,lo,hi,dtype", [
+    (8, 12, 2, 128, 48, 512, 4, 2048, 16384, torch.bfloat16),   # cfg4
+    (32, 16, 1, 96, 64, 1024, 8, 1024, 32768, torch.float16),   # cfg5
+])
+def test_decode_full_size_graph(cuda_device, batch, hq, hkv, d, page, chunk, topk, lo, hi, dtype):
+    """The captured step at the benchmark shapes: 24 graph replays on one
+    cache equal 24 eager steps on an identical cache bit for bit (outputs,
+    LSE, routes, and afterwards the closed-chunk means and lengths), with
+    eager work between the replays; rows 0 and 1 close a chunk during the run
+    (a closing mean inside the replayed graph).  The last replay is also
+    checked against the oracle."""
+    rng = random.Random(5)
+    lengths = [rng.randint(lo, hi) for _ in range(batch)]
+    lengths[0] = (lengths[0] // chunk) * chunk + chunk - 5   # closes a chunk at step 5
+    lengths[1] = (lengths[1] // chunk) * chunk + chunk - 17  # ... and at step 17
+    steps = 24
+    caches = [_decode_cache(batch, lengths, hkv, d, page, chunk, dtype, steps + 8, seed=31)
+              for _ in range(2)]
+    g = torch.Generator(device="cuda").manual_seed(32)
+    ids = list(range(batch))
+    with caches[0].prepare_decode(ids, hq, topk=topk) as pe, \
+            caches[1].prepare_decode(ids, hq, topk=topk) as pg:
+        pg.capture("step")
+        for step in range(steps):
+            q = torch.randn((batch, hq, d), generator=g, device="cuda").to(dtype)
+            kn = torch.randn((batch, hkv, d), generator=g, device="cuda").to(dtype)
+            vn = torch.randn((batch, hkv, d), generator=g, device="cuda").to(dtype)
+            a = pe.step(q, kn, vn)
+            _ = torch.randn(1000, device="cuda").sum().item()  # eager work between replays
+            b = pg.step(q, kn, vn, use_graph=True)
+            torch.cuda.synchronize()
+            assert torch.equal(a.output, b.output), f"step {step}: output"
+            assert torch.equal(a.lse, b.lse), f"step {step}: lse"
+            assert torch.equal(a.selected_blocks, b.selected_blocks), f"step {step}: routes"
+        check(caches[1], b, q)
+    ends = list(caches[1].lengths)
+    assert list(caches[0].lengths) == ends == [n + steps for n in lengths]
+    for row, n in enumerate(ends):  # the closed chunks' means (the rest is unwritten)
+        closed = n // chunk
+        assert torch.equal(caches[0]._means[row, :closed], caches[1]._means[row, :closed]), row
