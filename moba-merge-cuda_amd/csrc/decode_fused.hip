@@ -643,14 +643,14 @@ __global__ __launch_bounds__(64 * kMergeWaves) void merge_kernel(FusedArgs a) {
   const bool dok = d < a.D;
   float m[kMergePer], z[kMergePer];
   f32x4_t o[kMergePer];
-  // Every slot below smax is in the row's allocation: all loads are issued
-  // unconditionally, back to back, and slots past S (stale or uninitialised,
-  // possibly NaN) are dropped by a select afterwards.  Guarded loads compiled
+  // All loads are issued unconditionally, back to back, at slots clamped to
+  // the row's S (the repeats hit the cache, so only S slots' bytes move);
+  // slots past S are dropped by a select afterwards.  Guarded loads compiled
   // to one branch and one full wait per slot.
   const int dl = dok ? d : 0;
 #pragma unroll
   for (int i = 0; i < kMergePer; ++i) {
-    const int s = w + kMergeWaves * i;
+    const int s = min(w + kMergeWaves * i, S - 1);
     const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + 2 * (e0 + s));
     m[i] = ml.x;
     z[i] = ml.y;

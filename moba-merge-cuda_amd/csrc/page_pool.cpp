@@ -101,7 +101,8 @@ extern "C" int moba_pool_clone(const void* pool, void** out) {
 extern "C" int moba_pool_assign(void* dst, const void* src) {
   PagePool* d = as_pool(dst);
   const PagePool* s = as_pool(src);
-  if (!d || !s || d->batch != s->batch || d->width != s->width || d->num_pages != s->num_pages)
+  if (!d || !s || d->batch != s->batch || d->width != s->width || d->num_pages != s->num_pages ||
+      d->page != s->page || d->chunk != s->chunk || d->max_len != s->max_len)
     return arg_error("pool_assign: pools of different shapes");
   // element copies into the existing storage: views of table / lengths /
   // free stay valid
@@ -121,9 +122,15 @@ extern "C" int moba_pool_info(const void* pool, int64_t* info) {
   return MOBA_OK;
 }
 
-extern "C" const int32_t* moba_pool_table(const void* pool) { return as_pool(pool)->table.data(); }
-extern "C" const int32_t* moba_pool_lengths(const void* pool) { return as_pool(pool)->lengths.data(); }
-extern "C" const int32_t* moba_pool_free(const void* pool) { return as_pool(pool)->free.data(); }
+extern "C" const int32_t* moba_pool_table(const void* pool) {
+  return pool ? as_pool(pool)->table.data() : nullptr;
+}
+extern "C" const int32_t* moba_pool_lengths(const void* pool) {
+  return pool ? as_pool(pool)->lengths.data() : nullptr;
+}
+extern "C" const int32_t* moba_pool_free(const void* pool) {
+  return pool ? as_pool(pool)->free.data() : nullptr;
+}
 
 extern "C" int moba_pool_set_free(void* pool, const int32_t* pages, int n) {
   PagePool* p = as_pool(pool);
@@ -229,7 +236,11 @@ extern "C" int moba_pool_check_ids(const void* pool, const int32_t* ids, int n, 
 extern "C" int moba_pool_plan_step(const void* pool, const int32_t* ids, int n, int32_t* positions,
                                    int32_t* delta, int* n_grants, int64_t* version) {
   const PagePool* p = as_pool(pool);
-  if (!p || !n_grants || !version) return arg_error("pool_plan_step: null argument");
+  if (!p || !n_grants || !version || !delta || (n > 0 && !ids))
+    return arg_error("pool_plan_step: null argument");
+  // range only: a prepared step's ids were checked unique when it was made
+  for (int i = 0; i < n; ++i)
+    if (ids[i] < 0 || ids[i] >= p->batch) return arg_error("sequence ID outside cache batch slots");
   int need = 0;
   for (int i = 0; i < n; ++i) {
     const int pos = p->lengths[ids[i]];
@@ -254,7 +265,9 @@ extern "C" int moba_pool_plan_step(const void* pool, const int32_t* ids, int n, 
 extern "C" int moba_pool_commit_step(void* pool, const int32_t* ids, int n, const int32_t* delta,
                                      int64_t version) {
   PagePool* p = as_pool(pool);
-  if (!p) return arg_error("pool_commit_step: null pool");
+  if (!p || !delta || (n > 0 && !ids)) return arg_error("pool_commit_step: null argument");
+  for (int i = 0; i < n; ++i)
+    if (ids[i] < 0 || ids[i] >= p->batch) return arg_error("sequence ID outside cache batch slots");
   if (version != p->version) {
     moba_set_error("stale decode step plan");
     return MOBA_ERR_STALE;

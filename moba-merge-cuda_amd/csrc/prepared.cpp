@@ -134,6 +134,9 @@ extern "C" int moba_prep_schedule(const int32_t* positions, int rows, int hkv, i
   for (int k = 0; k < smax; ++k)
     for (int i = 0; i < r; ++i)
       if (k < s[i]) { entries[3 * e] = i; entries[3 * e + 1] = k; entries[3 * e + 2] = s[i]; ++e; }
+  // the launch has `total` workgroups and the kernels read the split counts
+  // after 3 * total entries: every workgroup must hold one
+  if (e != total) return fail(MOBA_ERR_ARG, "prep_schedule: workgroups not fully assigned");
   for (int i = 0; i < r; ++i) {
     entries[3 * e + i] = s[i];
     if (splits) splits[i] = s[i];

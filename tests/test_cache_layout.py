@@ -131,3 +131,34 @@ def test_fused_schedule_covers_every_split_once():
             for b in range(rows):
                 if w[a] > 1.5 * w[b] and splits[b] < 64:
                     assert splits[a] >= splits[b]
+
+
+def test_pool_c_abi_rejects_bad_ids_and_shapes():
+    """The C-ABI page pool checks what a direct caller could get wrong: step
+    ids outside the batch, pools of different geometry in assign, a null
+    pool in the view getters.  Nothing changes on a refused call."""
+    import ctypes
+    import numpy as np
+    from moba_hip.ops import _lib
+    lib = _lib.load()
+    pool, other = ctypes.c_void_p(), ctypes.c_void_p()
+    assert lib.moba_pool_create(2, 32, 4, 16, 8, ctypes.byref(pool)) == 0
+    assert lib.moba_pool_create(2, 32, 8, 16, 8, ctypes.byref(other)) == 0  # other page size
+    try:
+        ids = np.array([0, 5], dtype=np.int32)
+        delta = np.zeros(4, dtype=np.int32)
+        n_grants, version = ctypes.c_int(), ctypes.c_int64()
+        rc = lib.moba_pool_plan_step(pool, ids.ctypes.data, 2, None, delta.ctypes.data,
+                                     ctypes.byref(n_grants), ctypes.byref(version))
+        assert rc == _lib.MOBA_ERR_ARG
+        assert "outside cache batch slots" in lib.moba_hip_last_error().decode()
+        rc = lib.moba_pool_commit_step(pool, ids.ctypes.data, 2, delta.ctypes.data, 0)
+        assert rc == _lib.MOBA_ERR_ARG
+        assert lib.moba_pool_assign(pool, other) == _lib.MOBA_ERR_ARG
+        assert not lib.moba_pool_table(None) and not lib.moba_pool_lengths(None)
+        info = (ctypes.c_int64 * 8)()
+        assert lib.moba_pool_info(pool, info) == 0
+        assert info[6] == 0 and info[7] == 16  # version and free pages untouched
+    finally:
+        lib.moba_pool_destroy(pool)
+        lib.moba_pool_destroy(other)
