@@ -23,6 +23,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
+#include <utility>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -97,35 +98,30 @@ extern "C" int moba_prep_schedule(const int32_t* positions, int rows, int hkv, i
   for (int i = 0; i < r; ++i)
     w[i] = std::max(1.0, expected_tokens(std::max(0, (int)positions[i / hkv]), group, remote,
                                          chunk, dense != 0));
-  // largest-remainder shares of the free workgroups, each row in [1, max]
-  std::vector<int> s(r, 1), grant(r);
-  std::vector<double> share(r);
+  // Each row starts with one split; every further workgroup goes to the row
+  // whose expected tokens per split are largest (ties: lowest row), until
+  // the grid is used or every row has max_splits.  This minimises the
+  // largest per-workgroup share, which bounds the launch's tail.
+  std::vector<int> s(r, 1);
   int free = total - r;
-  std::vector<int> active(r);
-  for (int i = 0; i < r; ++i) active[i] = i;
-  while (free > 0 && !active.empty()) {
-    double wsum = 0;
-    for (int i : active) wsum += w[i];
-    int given = 0;
-    for (int i : active) {
-      share[i] = free * w[i] / wsum;
-      grant[i] = std::min((int)share[i], max_splits - s[i]);
-      given += grant[i];
+  std::vector<std::pair<double, int>> heap;
+  heap.reserve(r);
+  auto before = [](const std::pair<double, int>& x, const std::pair<double, int>& y) {
+    return x.first < y.first || (x.first == y.first && x.second > y.second);
+  };
+  for (int i = 0; i < r; ++i)
+    if (max_splits > 1) heap.emplace_back(w[i], i);
+  std::make_heap(heap.begin(), heap.end(), before);
+  while (free > 0 && !heap.empty()) {
+    std::pop_heap(heap.begin(), heap.end(), before);
+    const int i = heap.back().second;
+    heap.pop_back();
+    ++s[i];
+    --free;
+    if (s[i] < max_splits) {
+      heap.emplace_back(w[i] / s[i], i);
+      std::push_heap(heap.begin(), heap.end(), before);
     }
-    std::vector<int> order(active);
-    std::stable_sort(order.begin(), order.end(), [&](int a, int b) {
-      return share[a] - (int)share[a] > share[b] - (int)share[b];
-    });
-    for (int i : order) {
-      if (given >= free) break;
-      if (s[i] + grant[i] < max_splits) { ++grant[i]; ++given; }
-    }
-    for (int i : active) s[i] += grant[i];
-    free -= given;
-    std::vector<int> next;
-    for (int i : active) if (s[i] < max_splits) next.push_back(i);
-    if (given == 0) break;
-    active.swap(next);
   }
   // entries (row * hkv + kv head, split, splits), interleaved across rows so
   // one row's splits spread over the launch; then the split counts
