@@ -287,7 +287,7 @@ int moba_hip_decode_fused(const void* q, const void* k, const void* v, int dtype
  * capture, tight serving loops, harnesses that forbid hipMalloc).  No
  * counterpart in the reference.  Same as moba_hip_decode_fused with
  * pos_mode 0 (positions given; nothing in the cache changes) and the uniform
- * split count S = clamp(ceil(512 / (Nq*Hkv)), 1, 64), but the split partials
+ * split count S = clamp(ceil(256 / (Nq*Hkv)), 1, 64), but the split partials
  * live in a static per-device scratch array of 8 MiB instead of caller
  * workspaces: calls needing more than Nq*Hq*S*(D+2)*4 (+256) bytes fail
  * with MOBA_ERR_CAPACITY before launching anything.  It calls no allocating

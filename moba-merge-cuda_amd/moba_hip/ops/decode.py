@@ -73,12 +73,14 @@ def fused_supported(hq, hkv, d, width, table_width) -> bool:
 
 
 def fused_splits(nq, hkv) -> int:
-    """Workgroups per (row, kv head): about two per CU over the whole launch."""
-    return max(1, min(64, -(-512 // (nq * hkv))))
+    """Workgroups per (row, kv head): about one (8-wave workgroup) per CU
+    over the whole launch."""
+    return max(1, min(64, -(-SCHED_WORKGROUPS // (nq * hkv))))
 
 
-# Workgroups of a scheduled decode launch (two per CU) and the split cap.
-SCHED_WORKGROUPS = 512
+# Workgroups of a scheduled decode launch (one 8-wave workgroup per CU) and
+# the split cap.
+SCHED_WORKGROUPS = 256
 SCHED_MAX_SPLITS = 64
 
 
