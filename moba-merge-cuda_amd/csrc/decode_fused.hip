@@ -445,6 +445,12 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
   // K rows of tokens t0 + half*16 + c16 and the V rows of the block.  A row
   // is (source, element offset): the new token of a step comes from the input
   // row; tokens past the block end or on unmapped pages read as zero.
+  // The input rows are addressed as an element distance from the cache, so
+  // the per-lane choice of source is an integer add: a per-lane choice
+  // between the two argument pointers compiled to a load of the chosen
+  // pointer, and waiting for it also waited for every K/V load in flight.
+  const int64_t k_in_off = ((int64_t)(uintptr_t)a.k - (int64_t)(uintptr_t)a.kc) / 2;
+  const int64_t v_in_off = ((int64_t)(uintptr_t)a.v - (int64_t)(uintptr_t)a.vc) / 2;
   auto row_of = [&](int tok, bool& from_input) -> int64_t {
     from_input = false;
     if (tok >= 0 && step && tok == p) {
@@ -459,23 +465,25 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       const int tok = bk.t0 + half * 16 + c16;
-      bool inp;
+      bool inp = false;
       const int64_t base = tok < bk.t_end ? row_of(tok, inp) : -1;
-      const uint16_t* kp = inp ? a.k : a.kc;
+      const uint16_t* kp = a.kc + (inp ? k_in_off : 0);
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {
         const int d = ks * 32 + g4 * 8;
-        kr[half][ks] = (base >= 0 && d < D) ? ld8(kp + base + d) : zero8();
+        const bool ok = base >= 0 && d < D;
+        kr[half][ks] = ok ? ld8(kp + base + d) : zero8();
       }
     }
 #pragma unroll
     for (int x = 0; x < VLD; ++x) {
       const int id = lane + 64 * x, rr = id / (DP / 8), dc = (id % (DP / 8)) * 8;
       const int tok = bk.t0 + rr;
-      bool inp;
+      bool inp = false;
       const int64_t base = tok < bk.t_end ? row_of(tok, inp) : -1;
-      const uint16_t* vp = inp ? a.v : a.vc;
-      vr[x] = (base >= 0 && dc < D) ? ld8(vp + base + dc) : zero8();
+      const uint16_t* vp = a.vc + (inp ? v_in_off : 0);
+      const bool ok = base >= 0 && dc < D;
+      vr[x] = ok ? ld8(vp + base + dc) : zero8();
     }
   };
   auto compute = [&](const Blk& bk, const u16x8_t (&kr)[2][NKS], const u16x8_t (&vr)[VLD]) {
