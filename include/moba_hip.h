@@ -420,8 +420,9 @@ int64_t moba_prep_delta_uploads(const void* handle);
 /* Workgroups of a fused schedule: max(rows*hkv, min(workgroups, rows*hkv*max_splits)). */
 int moba_prep_sched_workgroups(int rows, int hkv, int workgroups, int max_splits);
 /* Split counts per (row, kv head) by the expected attended
- * tokens (each extra workgroup to the row with the most expected tokens per
- * split, each count in [1, max_splits]) over
+ * tokens plus the route each workgroup recomputes (each extra workgroup to
+ * the row with the most route + expected tokens per split, each count in
+ * [1, max_splits]) over
  * moba_prep_sched_workgroups workgroups: entries [3*n + rows*hkv] =
  * (row*hkv + kv head, split, splits) interleaved across rows, then the
  * counts; splits[rows*hkv] (nullable) the counts.  No counterpart in the

@@ -80,6 +80,17 @@ double expected_tokens(int pos, int group, int remote, int chunk, bool dense) {
   return own + chunk * cur * (1.0 - std::pow(1.0 - picks / cur, group));
 }
 
+// Fixed cost of one workgroup of a (row, kv head), in tokens of attention:
+// before it streams any K/V every workgroup recomputes the row's route, and
+// each (head, closed chunk) item of it costs about as much time as
+// kRouteTokensPerItem tokens of attention (route phases of the fused kernel
+// against its attention rate; 0.6 measured best of 0, 0.3, 0.6 and 1.2).
+constexpr double kRouteTokensPerItem = 0.6;
+double route_tokens(int pos, int group, int chunk, bool dense) {
+  if (dense) return 0.0;
+  return kRouteTokensPerItem * group * (pos / chunk);
+}
+
 }  // namespace
 
 extern "C" int moba_prep_sched_workgroups(int rows, int hkv, int workgroups, int max_splits) {
@@ -94,14 +105,17 @@ extern "C" int moba_prep_schedule(const int32_t* positions, int rows, int hkv, i
     return fail(MOBA_ERR_ARG, "prep_schedule: bad sizes");
   const int r = rows * hkv;
   const int total = moba_prep_sched_workgroups(rows, hkv, workgroups, max_splits);
-  std::vector<double> w(r);
-  for (int i = 0; i < r; ++i)
-    w[i] = std::max(1.0, expected_tokens(std::max(0, (int)positions[i / hkv]), group, remote,
-                                         chunk, dense != 0));
+  std::vector<double> w(r), f(r);
+  for (int i = 0; i < r; ++i) {
+    const int pos = std::max(0, (int)positions[i / hkv]);
+    w[i] = std::max(1.0, expected_tokens(pos, group, remote, chunk, dense != 0));
+    f[i] = route_tokens(pos, group, chunk, dense != 0);
+  }
   // Each row starts with one split; every further workgroup goes to the row
-  // whose expected tokens per split are largest (ties: lowest row), until
-  // the grid is used or every row has max_splits.  This minimises the
-  // largest per-workgroup share, which bounds the launch's tail.
+  // whose workgroups have the most to do, route plus expected tokens per
+  // split (ties: lowest row), until the grid is used or every row has
+  // max_splits.  This minimises the largest per-workgroup time, which
+  // bounds the launch's tail.
   std::vector<int> s(r, 1);
   int free = total - r;
   std::vector<std::pair<double, int>> heap;
@@ -110,7 +124,7 @@ extern "C" int moba_prep_schedule(const int32_t* positions, int rows, int hkv, i
     return x.first < y.first || (x.first == y.first && x.second > y.second);
   };
   for (int i = 0; i < r; ++i)
-    if (max_splits > 1) heap.emplace_back(w[i], i);
+    if (max_splits > 1) heap.emplace_back(f[i] + w[i], i);
   std::make_heap(heap.begin(), heap.end(), before);
   while (free > 0 && !heap.empty()) {
     std::pop_heap(heap.begin(), heap.end(), before);
@@ -119,7 +133,7 @@ extern "C" int moba_prep_schedule(const int32_t* positions, int rows, int hkv, i
     ++s[i];
     --free;
     if (s[i] < max_splits) {
-      heap.emplace_back(w[i] / s[i], i);
+      heap.emplace_back(f[i] + w[i] / s[i], i);
       std::push_heap(heap.begin(), heap.end(), before);
     }
   }

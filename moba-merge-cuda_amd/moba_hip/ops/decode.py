@@ -109,9 +109,11 @@ def fused_schedule(positions, hkv, group, remote, chunk, dense=False,
                    workgroups=SCHED_WORKGROUPS, max_splits=SCHED_MAX_SPLITS):
     """The split schedule the prepared-decode driver uploads (computed by
     ``moba_prep_schedule``): split counts per (row, kv head) by the expected
-    attended tokens (``expected_union_tokens``; each workgroup beyond one per
-    row goes to the row with the most expected tokens per split, each count
-    in [1, max_splits]) over exactly ``sched_workgroups`` workgroups.  Returns (schedule int32 list: the workgroup entries
+    attended tokens (``expected_union_tokens``) plus the route every
+    workgroup recomputes (0.6 tokens per (q head, closed chunk)); each
+    workgroup beyond one per row goes to the row whose workgroups carry the
+    most (route + expected tokens per split), each count in [1, max_splits],
+    over exactly ``sched_workgroups`` workgroups.  Returns (schedule int32 list: the workgroup entries
     (row * hkv + kv head, split, splits of that row) interleaved across rows,
     then the split counts; the split counts; the number of workgroups)."""
     import numpy as np
