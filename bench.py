@@ -394,7 +394,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one MI355X: multi-GPU runs are not part of this build "
-              "(the path shards by KV-head group / request with no collective; see DESIGN.md)",
+              "(the path would shard by KV-head group or request, with no collective)",
               file=sys.stderr)
         sys.exit(2)
     import torch
