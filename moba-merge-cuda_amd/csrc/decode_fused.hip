@@ -56,11 +56,20 @@ extern "C" int moba_decode_trace_read(void* dst) {
 
 namespace {
 
-// Waves per workgroup.  Eight waves (one workgroup per CU, 256 workgroups
-// over the chip) run the route's (head, chunk) items in one pass of 512
+// Waves per workgroup (one workgroup per CU, 256 workgroups over the
+// chip).  Eight waves run the route's (head, chunk) items in one pass of 512
 // threads where four waves needed two, and halve the split partials the
-// merge reads: cfg5 steps 68.0 -> 65.9 us, cfg4 unchanged.
-constexpr int kFW = 8;
+// merge reads against 4-wave workgroups two per CU (cfg5 68.0 -> 65.9 us).
+// Each of them streams its blocks through two register buffers (251
+// registers, 2 waves per SIMD).  A launch whose workgroups carry many blocks
+// instead takes 12 waves of one buffer each (167 registers, 3 waves per
+// SIMD): with one block's load latency exposed per block either way, 1.5
+// times the waves keep 1.5 times the bytes in flight (cfg5 64.5 -> 62.6 us;
+// cfg4, about 4 blocks per workgroup, 26.0 -> 26.8 us with 12 waves, so it
+// keeps 8).  D > 128 keeps 8 waves: 12 V tiles of 256 dims exceed LDS.
+constexpr int kFwNarrow = 8;
+constexpr int kFwWide = 12;
+constexpr int kWideBlocksPerWorkgroup = 16;  // expected blocks at which 12 waves pay
 constexpr int kMaxSlots = 9;    // current chunk + up to 8 routed chunks
 constexpr int kTblMax = 2048;   // page-table entries staged in LDS
 
@@ -96,15 +105,29 @@ inline size_t fused_route_lds(int G, int width) {
          ((size_t)G * width + 3 * (size_t)(width + 1) + (width + 2) + 16 * kMaxSlots + kTblMax);
 }
 
-template <int DT, int DP>
-__global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
+// Static LDS of fused_kernel<., DP, FW>: the per-wave V tiles (rows of
+// DP + 8 elements), aliased after the attention by the waves' partials
+// (rows of DP + 4 floats: float4 stores of 16 lanes hit 16 distinct bank
+// groups).
+constexpr size_t fused_static_lds(int DP, int FW) {
+  return (size_t)FW * 32 * (DP + 8) * 2 > (size_t)FW * (16 * (DP + 4) + 32) * 4
+             ? (size_t)FW * 32 * (DP + 8) * 2
+             : (size_t)FW * (16 * (DP + 4) + 32) * 4;
+}
+constexpr size_t kLdsBytes = 160 * 1024;
+
+template <int DT, int DP, int FW>
+__global__ __launch_bounds__(64 * FW) void fused_kernel(FusedArgs a) {
+  constexpr int kFW = FW;
   constexpr int NKS = DP / 32;  // 32-d k-steps of S^T
   constexpr int NDB = DP / 16;  // 16-d blocks of O^T
   constexpr int VS = DP + 8;
   constexpr int STAGE = 32 * VS;  // per-wave V tile (elements)
   constexpr int STAGE_BYTES = kFW * STAGE * 2;
-  constexpr int WS = DP + 4;  // merge row stride (floats): float4 stores of 16 lanes hit 16 distinct bank groups
+  constexpr int WS = DP + 4;
   constexpr int MERGE_BYTES = kFW * (16 * WS + 32) * 4;
+  static_assert(fused_static_lds(DP, FW) == (STAGE_BYTES > MERGE_BYTES ? STAGE_BYTES : MERGE_BYTES),
+                "static LDS size");
   constexpr int VLD = 32 * (DP / 8) / 64;  // 16-byte V chunks per lane per block
   static_assert(64 * (DP + 8) * 2 + 16 * DP * 4 <= (STAGE_BYTES > MERGE_BYTES ? STAGE_BYTES : MERGE_BYTES),
                 "route staging must fit the V-tile / merge buffer");
@@ -550,8 +573,15 @@ __global__ __launch_bounds__(64 * kFW) void fused_kernel(FusedArgs a) {
   {
     // ping-pong register buffers: block b + 4 loads while block b computes
     int b = b0 + w;
-    if (b < b1) {
-      u16x8_t kA[2][NKS], vA[VLD], kB[2][NKS], vB[VLD];
+    if constexpr (FW > kFwNarrow) {
+      // one register buffer: load, then compute, block after block
+      for (; b < b1; b += kFW) {
+        u16x8_t kA[2][NKS], vA[VLD];
+        const Blk bA = block_info(b);
+        load(bA, kA, vA);
+        compute(bA, kA, vA);
+      }
+    } else if (b < b1) {      u16x8_t kA[2][NKS], vA[VLD], kB[2][NKS], vB[VLD];
       Blk bA = block_info(b), bB;
       load(bA, kA, vA);
       __builtin_amdgcn_sched_barrier(0);
@@ -721,11 +751,27 @@ __global__ __launch_bounds__(64 * kMergeWaves) void merge_kernel(FusedArgs a) {
   }
 }
 
+// Whether the launch's workgroups carry enough 32-token blocks for the
+// 12-wave form: at most min(width, R + 1) chunks of C / 32 blocks per
+// (row, kv head) (every chunk when dense), over that row's workgroups.
+bool wide_launch(const FusedArgs& a, int splits, int DP, size_t dyn) {
+  if (dyn + fused_static_lds(DP, kFwWide) > kLdsBytes) return false;
+  const int64_t chunks = a.dense ? a.width : std::min(a.width, a.R + 1);
+  const int64_t blocks = chunks * ((a.C + 31) / 32);
+  const int64_t per_row = a.sched != nullptr ? std::max(1, a.n_sched / (a.Nq * a.Hkv)) : splits;
+  return blocks >= (int64_t)kWideBlocksPerWorkgroup * per_row;
+}
+
 template <int DT, int DP>
 int launch_fused(const FusedArgs& a, int splits, size_t dyn, hipStream_t st) {
   const dim3 grid = a.sched != nullptr ? dim3((unsigned)a.n_sched)
                                         : dim3((unsigned)splits, (unsigned)(a.Nq * a.Hkv));
-  hipLaunchKernelGGL((fused_kernel<DT, DP>), grid, dim3(64 * kFW), dyn, st, a);
+  bool wide = false;
+  if constexpr (DP <= 128) {
+    wide = wide_launch(a, splits, DP, dyn);
+    if (wide) hipLaunchKernelGGL((fused_kernel<DT, DP, kFwWide>), grid, dim3(64 * kFwWide), dyn, st, a);
+  }
+  if (!wide) hipLaunchKernelGGL((fused_kernel<DT, DP, kFwNarrow>), grid, dim3(64 * kFwNarrow), dyn, st, a);
   hipLaunchKernelGGL((merge_kernel<DT>), dim3((unsigned)(a.Nq * a.Hq)), dim3(64 * kMergeWaves), 0, st, a);
   return moba_launch_status("decode_fused");
 }
@@ -756,7 +802,9 @@ int uniform_splits(int Nq, int Hkv) {
 extern "C" int moba_hip_decode_fused_supported(int Hq, int Hkv, int D, int width, int table_width) {
   if (Hkv < 1 || Hq % Hkv || Hq / Hkv > 16 || D % 8 || D < 8 || D > 256) return 0;
   if (table_width < 1 || table_width > kTblMax) return 0;
-  return fused_route_lds(Hq / Hkv, width) <= 64 * 1024 ? 1 : 0;
+  const int DP = D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 256;
+  const size_t dyn = fused_route_lds(Hq / Hkv, width);
+  return dyn <= 64 * 1024 && dyn + fused_static_lds(DP, kFwNarrow) <= kLdsBytes ? 1 : 0;
 }
 
 extern "C" int moba_hip_decode_fused(const void* q, const void* k, const void* v, int dtype, int Nq,
