@@ -324,7 +324,7 @@ __global__ __launch_bounds__(64 * FW) void fused_kernel(FusedArgs a) {
         // operands of 8 pieces (64 d) are read in one batch, then the chain
         // runs on registers; pieces past D are zero in both rows, and
         // fma(0, 0, acc) == acc
-        constexpr int JB = RC < 8 ? RC : 8;
+        constexpr int JB = RC % 8 == 0 ? 8 : RC % 6 == 0 ? 6 : RC;  // divides RC
 #pragma unroll
         for (int j0 = 0; j0 < RC; j0 += JB) {
           u16x8_t mv[JB];
@@ -780,6 +780,7 @@ template <int DT>
 int dispatch_fused(const FusedArgs& a, int splits, size_t dyn, hipStream_t st) {
   if (a.D <= 32) return launch_fused<DT, 32>(a, splits, dyn, st);
   if (a.D <= 64) return launch_fused<DT, 64>(a, splits, dyn, st);
+  if (a.D <= 96) return launch_fused<DT, 96>(a, splits, dyn, st);
   if (a.D <= 128) return launch_fused<DT, 128>(a, splits, dyn, st);
   return launch_fused<DT, 256>(a, splits, dyn, st);
 }
@@ -802,7 +803,7 @@ int uniform_splits(int Nq, int Hkv) {
 extern "C" int moba_hip_decode_fused_supported(int Hq, int Hkv, int D, int width, int table_width) {
   if (Hkv < 1 || Hq % Hkv || Hq / Hkv > 16 || D % 8 || D < 8 || D > 256) return 0;
   if (table_width < 1 || table_width > kTblMax) return 0;
-  const int DP = D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 256;
+  const int DP = D <= 32 ? 32 : D <= 64 ? 64 : D <= 96 ? 96 : D <= 128 ? 128 : 256;
   const size_t dyn = fused_route_lds(Hq / Hkv, width);
   return dyn <= 64 * 1024 && dyn + fused_static_lds(DP, kFwNarrow) <= kLdsBytes ? 1 : 0;
 }
