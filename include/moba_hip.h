@@ -259,6 +259,9 @@ int moba_hip_decode_fused_supported(int Hq, int Hkv, int D, int width, int table
  * and lse [Nq,Hq] fp32 natural log.
  * pos_mode 0: positions [Nq] are given (read only; no table, length or pool
  *             change).
+ * ids [Nq] maps rows to cache slots (pos_mode 1 and 2); null means row i is
+ *             slot i, which saves the kernel a dependent load before the
+ *             position is known.
  * pos_mode 1: position = lengths[ids[row]] - 1 (prepared attend); the
  *             page-table delta [2,Nq] (logical, physical; -1 = none; may be
  *             null) is applied; positions written.

@@ -150,7 +150,7 @@ __global__ __launch_bounds__(64 * FW) void fused_kernel(FusedArgs a) {
   // Row state comes from uniform (scalar) loads; the loads that need only the
   // slot (q rows, the first 64 closed-chunk means, the page-table row) are
   // issued before the position is known, so they overlap the lengths load.
-  const int sid = a.ids[qrow];
+  const int sid = a.ids != nullptr ? a.ids[qrow] : qrow;  // null ids: row i is slot i
   const int* trow = a.table + (int64_t)sid * a.W;
   int* tbl = dyn + (G * width + 3 * (width + 1) + (width + 2) + 16 * kMaxSlots);
   constexpr int RC = DP / 8;                  // 16-byte pieces per row
@@ -747,7 +747,7 @@ __global__ __launch_bounds__(64 * kMergeWaves) void merge_kernel(FusedArgs a) {
   }
   if (lane == 0) {
     a.lse[rh] = (M + log2f(Z)) * kLn2;
-    if (a.pos_mode == 2 && h == 0) a.lengths[a.ids[qrow]] = p + 1;
+    if (a.pos_mode == 2 && h == 0) a.lengths[a.ids != nullptr ? a.ids[qrow] : qrow] = p + 1;
   }
 }
 

@@ -41,6 +41,7 @@ constexpr int kRing = 16;  // pinned delta staging slots
 struct Prepared {
   MobaPrepDesc d;
   std::vector<int32_t> ids;
+  bool ids_identity = false;  // row i is slot i: the fused launch skips the ids load
   int32_t* pinned = nullptr;       // [kRing][2 * rows] delta staging, then the schedule
   int32_t* sched_pinned = nullptr;
   hipEvent_t ring_ev[kRing] = {};
@@ -163,7 +164,8 @@ int launch(Prepared& p, bool append, hipStream_t st) {
   if (d.fused) {
     return moba_hip_decode_fused(d.q, append ? d.k : nullptr, append ? d.v : nullptr, d.dtype,
                                  d.rows, d.hq, d.hkv, d.head_dim, d.k_cache, d.v_cache,
-                                 d.page_size, d.table, d.table_width, d.lengths, d.ids_dev,
+                                 d.page_size, d.table, d.table_width, d.lengths,
+                                 p.ids_identity ? nullptr : d.ids_dev,
                                  d.positions, d.delta, d.means, d.max_chunks, d.chunk, d.width,
                                  d.remote, d.dense, append ? 2 : 1, d.splits, d.sched, d.n_sched,
                                  d.dense ? nullptr : d.selected, d.part_o, d.part_ml, d.out,
@@ -254,6 +256,8 @@ extern "C" int moba_prep_create(const MobaPrepDesc* desc, const int32_t* ids, vo
   if (!p) return fail(MOBA_ERR_ARG, "prep_create: out of host memory");
   p->d = d;
   p->ids.assign(ids, ids + d.rows);
+  p->ids_identity = true;
+  for (int i = 0; i < d.rows; ++i) p->ids_identity = p->ids_identity && ids[i] == i;
   p->delta.assign(2 * d.rows, -1);
   const size_t ring = (size_t)kRing * 2 * d.rows;
   const size_t sched = d.fused && d.sched ? (size_t)3 * d.n_sched + d.rows * d.hkv : 0;
