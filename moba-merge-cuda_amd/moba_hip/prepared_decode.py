@@ -164,18 +164,19 @@ class PreparedDecode:
 
     # ------------------------------------------------------------- checks
     def _usable(self):
-        """Lifecycle and stream checks; returns the cache stream."""
+        """Lifecycle and stream checks; returns the cache stream.  (Plain
+        tests: this runs on every step, whose host time bounds graph
+        replays.)"""
         c = self.cache
-        _require([(lambda: not self.closed and c._lessee is self,
-                   "prepared decode is closed or no longer owns cache")])
+        if self.closed or c._lessee is not self:
+            raise ValueError("prepared decode is closed or no longer owns cache")
         if self.failed:
             raise RuntimeError("CUDA execution failed; discard prepared decode and cache")
         stream = _raw_stream(self._dev)
-        _require([
-            (lambda: not torch.cuda.is_current_stream_capturing(),
-             "use capture(), not external capture"),
-            (lambda: stream == c._stream, "cross-stream cache access is unsupported"),
-        ])
+        if torch.cuda.is_current_stream_capturing():
+            raise ValueError("use capture(), not external capture")
+        if stream != c._stream:
+            raise ValueError("cross-stream cache access is unsupported")
         return stream
 
     def _bind(self, given, buffer, name):
@@ -251,18 +252,24 @@ class PreparedDecode:
                 self.q.copy_(q)
             return self._result(self._run(False, use_graph, stream))
 
-    @torch.no_grad()
     def step(self, q, k, v, *, use_graph=False):
         """One token per leased row; argument and capacity errors change nothing."""
         with self.cache._lock:
             stream = self._usable()
+            if q is self.q and k is self.k and v is self.v and not self.check_finite:
+                # the bound buffers are the inputs: plan, launch and commit
+                # in one native call
+                if use_graph and "step" not in self._captured:
+                    raise ValueError("capture('step') first")
+                return self._result(self._run(True, use_graph, stream))
             copies = [(t, b) for t, b, n in ((q, self.q, "q"), (k, self.k, "k"), (v, self.v, "v"))
                       if self._bind(t, b, n)]
             if use_graph and "step" not in self._captured:
                 raise ValueError("capture('step') first")
             positions = self._plan_step(stream)  # refuses (ValueError) before any change
-            for given, buffer in copies:
-                buffer.copy_(given)
+            with torch.no_grad():
+                for given, buffer in copies:
+                    buffer.copy_(given)
             lib = _lib.load()
             if lib.moba_prep_launch(self._handle, 1, int(use_graph), stream) or \
                     lib.moba_prep_commit(self._handle):
