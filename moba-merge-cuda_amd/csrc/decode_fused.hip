@@ -581,7 +581,8 @@ __global__ __launch_bounds__(64 * FW) void fused_kernel(FusedArgs a) {
         load(bA, kA, vA);
         compute(bA, kA, vA);
       }
-    } else if (b < b1) {      u16x8_t kA[2][NKS], vA[VLD], kB[2][NKS], vB[VLD];
+    } else if (b < b1) {
+      u16x8_t kA[2][NKS], vA[VLD], kB[2][NKS], vB[VLD];
       Blk bA = block_info(b), bB;
       load(bA, kA, vA);
       __builtin_amdgcn_sched_barrier(0);
