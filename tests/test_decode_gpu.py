@@ -54,6 +54,32 @@ def test_decode_head_dimensions(cuda_device, dim, dtype):
                                   mode=mode), q)
 
 
+@pytest.mark.parametrize("dim", [32, 64, 96, 128])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_decode_twelve_wave_launch(cuda_device, dim, dtype):
+    """Launches whose workgroups carry at least 16 blocks take the 12-wave,
+    single-buffered form of the fused kernel: 32 rows x 4 kv heads leave 2
+    splits per (row, kv head) over the 256 workgroups, and top-2 routing at
+    chunk 512 gives 2 x 16 blocks per row.  Attend and append-and-attend
+    against the oracle at every head dim that form is built for."""
+    from moba_hip.ops import decode as DK
+    Paged, _ = _caches()
+    B, hk, hq, C = 32, 4, 16, 512
+    lengths = [1024 + 37 * i for i in range(B)]
+    cu = [0]
+    for n in lengths:
+        cu.append(cu[-1] + n)
+    assert 2 * (C // 32) >= 16 * DK.fused_splits(B, hk)  # the 12-wave condition
+    cache = Paged(B, 2304, hk, dim, page_size=48, chunk_size=C, dtype=dtype)
+    k, v = rand((cu[-1], hk, dim), dtype, 141), rand((cu[-1], hk, dim), dtype, 142)
+    rows = list(range(B))
+    cache.append(k, v, sequence_ids=rows, cu_seqlens=cu)
+    q = rand((B, hq, dim), dtype, 143)
+    check(cache, cache.attend(q, sequence_ids=rows, topk=2), q)
+    kn, vn = rand((B, hk, dim), dtype, 144), rand((B, hk, dim), dtype, 145)
+    check(cache, cache.append_and_attend(q, kn, vn, sequence_ids=rows, topk=2), q)
+
+
 @pytest.mark.parametrize("dim", [1, 3, 7, 33, 65, 95, 129, 255])
 def test_decode_unaligned_head_dimensions(cuda_device, dim):
     Paged, _ = _caches()
