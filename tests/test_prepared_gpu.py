@@ -167,6 +167,44 @@ def test_graph_replays_match_eager(cuda_device):
             assert torch.equal(a.selected_blocks, b.selected_blocks)
 
 
+def test_bound_buffer_steps_match_copied_inputs(cuda_device):
+    """step() with the plan's own q / k / v buffers as the inputs takes one
+    native call (plan, launch, commit) instead of staging copies; eager and
+    graph steps must give the same outputs, routes, positions and cache
+    contents as steps whose inputs are separate tensors."""
+    dtype = torch.bfloat16
+    P = _paged()
+    copied = P(2, 200, 2, 64, page_size=5, chunk_size=8, dtype=dtype)
+    bound = P(2, 200, 2, 64, page_size=5, chunk_size=8, dtype=dtype)
+    k, v = rand((90, 2, 64), dtype, 961), rand((90, 2, 64), dtype, 962)
+    for c in (copied, bound):
+        c.append(k, v, sequence_ids=[0, 1], cu_seqlens=[0, 40, 90])
+    with copied.prepare_decode([1, 0], 12, topk=4, check_finite=False) as pc, \
+            bound.prepare_decode([1, 0], 12, topk=4, check_finite=False) as pb:
+        with pytest.raises(ValueError, match="capture"):
+            pb.step(pb.q, pb.k, pb.v, use_graph=True)
+        pc.capture("step")
+        pb.capture("step")
+        for step in range(10):
+            graph = step >= 5
+            q = rand((2, 12, 64), dtype, 970 + step)
+            kn, vn = rand((2, 2, 64), dtype, 980 + step), rand((2, 2, 64), dtype, 990 + step)
+            a = pc.step(q, kn, vn, use_graph=graph)
+            pb.q.copy_(q)
+            pb.k.copy_(kn)
+            pb.v.copy_(vn)
+            b = pb.step(pb.q, pb.k, pb.v, use_graph=graph)
+            torch.cuda.synchronize()
+            assert a.positions == b.positions
+            assert torch.equal(a.output, b.output) and torch.equal(a.lse, b.lse)
+            assert torch.equal(a.selected_blocks, b.selected_blocks)
+        assert pc.lengths == pb.lengths
+    for sid in range(2):
+        ka, va = copied.materialize(sid)
+        kb, vb = bound.materialize(sid)
+        assert torch.equal(ka, kb) and torch.equal(va, vb)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_prepared_route_ties_pick_lowest_chunks(cuda_device, dtype):
     """Constant keys make every closed chunk's gate score equal: the fused
