@@ -571,7 +571,9 @@ __global__ __launch_bounds__(64 * FW) void fused_kernel(FusedArgs a) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   };
   {
-    // ping-pong register buffers: block b + 4 loads while block b computes
+    // wave w takes blocks b0 + w, b0 + w + kFW, ...: 12-wave form one
+    // register buffer, 8-wave form two (ping-pong: block b + kFW loads while
+    // block b computes)
     int b = b0 + w;
     if constexpr (FW > kFwNarrow) {
       // one register buffer: load, then compute, block after block
@@ -781,6 +783,7 @@ template <int DT>
 int dispatch_fused(const FusedArgs& a, int splits, size_t dyn, hipStream_t st) {
   if (a.D <= 32) return launch_fused<DT, 32>(a, splits, dyn, st);
   if (a.D <= 64) return launch_fused<DT, 64>(a, splits, dyn, st);
+  // 96 wide: 3 k-steps / 6 d blocks instead of a masked quarter of 128
   if (a.D <= 96) return launch_fused<DT, 96>(a, splits, dyn, st);
   if (a.D <= 128) return launch_fused<DT, 128>(a, splits, dyn, st);
   return launch_fused<DT, 256>(a, splits, dyn, st);
