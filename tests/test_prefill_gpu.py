@@ -209,3 +209,22 @@ def test_opt_merge_hip_registry_entry(cuda_device, dtype):
         moba_hip.run_impl("opt_merge_hip", q, kg, vg, cu, ml, cfg)
     # the GQA entry accepts the same tensors
     moba_hip.run_impl("opt_hip", q, kg, vg, cu, ml, cfg)
+
+
+def test_cu_seqlens_in_place_write_is_seen(cuda_device):
+    """The host copy of cu_seqlens is reused only while the tensor is
+    unchanged: an in-place write (new split, same total) changes the routes
+    like a fresh tensor does, and an invalid in-place write is rejected."""
+    import moba_hip
+    hq, D, C, K = 4, 64, 32, 2
+    q, k, v, cu, ml, _ = prefill_inputs(hq, 2, D, (200, 120), torch.bfloat16, seed=23)
+    cfg = {"chunk_size": C, "topk": K}
+    first = moba_hip.run_impl("opt_hip", q, k, v, cu, ml, cfg)
+    cu.copy_(torch.tensor([0, 64, 320], dtype=torch.int32))
+    second = moba_hip.run_impl("opt_hip", q, k, v, cu, 256, cfg)
+    fresh = moba_hip.run_impl("opt_hip", q, k, v, cu.clone(), 256, cfg)
+    assert torch.equal(second, fresh)
+    assert not torch.equal(second, first)
+    cu[1] = 0
+    with pytest.raises(ValueError, match="strictly increase"):
+        moba_hip.run_impl("opt_hip", q, k, v, cu, 320, cfg)
