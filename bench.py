@@ -131,7 +131,9 @@ def bench_prefill(steps, warmup, seed):
     for c in cases:
         for _ in range(warmup):
             c.step()
-    rounds = max(1, min(5, steps))
+    # at least 4 steps per round: the first step after a synchronisation also
+    # carries the host's launch latency, and the round median passes over it
+    rounds = max(1, min(5, steps // 4))
     per = [steps // rounds + (1 if r < steps % rounds else 0) for r in range(rounds)]
     res = {c.name: {"round_medians": [], "steps": [], "wall": 0.0} for c in cases}
     dkdv = []
