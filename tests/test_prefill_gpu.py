@@ -91,6 +91,10 @@ def test_routing_bit_exact(cuda_device, hq, hkv, dim, lens, chunk, topk, dtype, 
     (6, 2, 72, (200, 7), 24, 9),
     (8, 1, 64, (35, 62), 16, 1),
     (8, 1, 64, (1, 3), 16, 4),
+    # the smallest head dim, and dims padded inside the 128- and 256-wide kernels
+    (4, 4, 8, (70, 33), 16, 3),
+    (6, 2, 96, (130, 61), 32, 3),
+    (4, 2, 192, (90, 41), 16, 4),
 ])
 def test_forward_backward_vs_fp64(cuda_device, hq, hkv, dim, lens, chunk, topk, dtype):
     q, k, v, cu, ml, g = prefill_inputs(hq, hkv, dim, lens, dtype, seed=62)
