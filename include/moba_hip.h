@@ -89,8 +89,10 @@ int moba_hip_prefill_rows(int D);
  * Replaces OptMixedAttention.forward (src/moba_opt/mixed_attention.py:42-139):
  * both _flash_attn_varlen_forward calls and merge_forward_cuda
  * (src/moba_opt/ops/merge.cu:187-288).
- * q [T,Hq,D], k/v [T,Hkv,D]; self_tiles[n_self_tiles][2] = (chunk, first row)
- * tiles of moba_hip_prefill_rows(D) rows; sel/R, filtered[F] and the pack_experts outputs (with
+ * q [T,Hq,D], k/v [T,Hkv,D]; self_tiles[n_self_tiles][3] = (chunk, first row,
+ * kv head) tiles of moba_hip_prefill_rows(D) rows, chunk -1 for an empty entry;
+ * the G workgroups of entries [x*n/8, (x+1)*n/8) run on XCD x when n is a
+ * multiple of 8 (any list is correct; this layout keeps a run in one L2); sel/R, filtered[F] and the pack_experts outputs (with
  * block_rows = moba_hip_prefill_rows(D)) describe
  * the remote rows (R = 0: self branch only, e.g. the full-causal fallback with
  * one chunk per sequence).  max_remote_tiles bounds tile_off[E].

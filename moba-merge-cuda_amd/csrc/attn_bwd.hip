@@ -104,18 +104,24 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a
       h[qb] = sh % a.Hq;
     }
   } else {
-    // grid (q head within the kv group, tile, kv head): the G heads that
-    // share a kv head's K/V run next to each other, then the next tile of the
-    // same kv head (tiles listed largest first)
-    const int c = a.self_tiles[2 * blockIdx.y], row0 = a.self_tiles[2 * blockIdx.y + 1];
-    kh = blockIdx.z;
+    // 1-D grid over (tile, q head within the kv group), tiles in the
+    // host's order of 8 XCD runs: workgroup L runs on XCD L % 8 and takes
+    // entry xcd_contiguous(L) / G, so each run's tiles share that XCD's L2.
+    // Entries are (chunk, first row, kv head); chunk -1 pads a run.
+    const int t = xcd_contiguous(blockIdx.x, a.n_self_wg);
+    if (t < 0) return;
+    const int e = t / a.G, g = t - e * a.G;
+    const int c = a.self_tiles[3 * e];
+    if (c < 0) return;
+    const int row0 = a.self_tiles[3 * e + 1];
+    kh = a.self_tiles[3 * e + 2];
     k_lo = a.cu_chunk[c];
     const int c_end = a.cu_chunk[c + 1];
     k_hi = min(c_end, k_lo + row0 + 128 * QB);
     s_wave0 = k_lo + row0 + wave * (32 * QB);
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-      h[qb] = blockIdx.z * a.G + blockIdx.x;
+      h[qb] = kh * a.G + g;
       s[qb] = s_wave0 + qb * 32 + qi;
       valid[qb] = s[qb] < c_end;
       if (!valid[qb]) s[qb] = k_hi - 1;
@@ -922,7 +928,7 @@ int launch_bwd(const BwdArgs& a, int n_self, int n_kv, int max_remote, int parts
     if (max_remote > 0 && a.R > 0)
       hipLaunchKernelGGL((dq_kernel<DT, DP, true, attn_qb<DP>()>), dim3((max_remote + 7) / 8 * 8), dim3(256), 0, st, a);
     if (n_self > 0)
-      hipLaunchKernelGGL((dq_kernel<DT, DP, false, attn_qb<DP>()>), dim3(a.G, n_self, a.Hkv), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((dq_kernel<DT, DP, false, attn_qb<DP>()>), dim3((unsigned)(((int64_t)n_self * a.G + 7) / 8 * 8)), dim3(256), 0, st, a);
   }
   if ((parts & 2) && n_kv > 0) {
     // kKvTileKeys keys per workgroup in every kernel; the host's key tiles match
@@ -979,7 +985,7 @@ extern "C" int moba_hip_prefill_bwd(const void* q, const void* k, const void* v,
   if (D < 8 || D > 256 || D % 8) { moba_set_error("prefill_bwd: head_dim must be a multiple of 8 in [8,256]"); return MOBA_ERR_ARG; }
   if (Hq < 1 || Hkv < 1 || Hq % Hkv) { moba_set_error("prefill_bwd: Hq must be a positive multiple of Hkv"); return MOBA_ERR_ARG; }
   if (R < 0 || R > 8) { moba_set_error("prefill_bwd: remote count must be in [0,8]"); return MOBA_ERR_ARG; }
-  if (n_self_tiles > 65535 || Hq > 65535) { moba_set_error("prefill_bwd: too many heads or self tiles"); return MOBA_ERR_ARG; }
+  if (Hq > 65535 || (int64_t)n_self_tiles * (Hq / Hkv) > (1 << 30)) { moba_set_error("prefill_bwd: too many heads or self tiles"); return MOBA_ERR_ARG; }
   if (parts < 1 || parts > 3) { moba_set_error("prefill_bwd: parts must be 1 (dq), 2 (dk/dv) or 3 (both)"); return MOBA_ERR_ARG; }
   if ((int64_t)T * Hq * D * 2 >= ((int64_t)1 << 32)) { moba_set_error("prefill_bwd: q / dO must be smaller than 4 GiB (32-bit buffer offsets)"); return MOBA_ERR_ARG; }
   if (kv_splits < 1 || kv_splits > 16 || (kv_splits > 1 && part_dkv == nullptr)) { moba_set_error("prefill_bwd: kv_splits must be in [1,16], with a part_dkv workspace when > 1"); return MOBA_ERR_ARG; }
@@ -991,6 +997,7 @@ extern "C" int moba_hip_prefill_bwd(const void* q, const void* k, const void* v,
   a.T = T; a.Hq = Hq; a.Hkv = Hkv; a.D = D; a.G = Hq / Hkv;
   a.scale = scale; a.scale_log2 = scale * kLog2e;
   a.cu_chunk = cu_chunk; a.self_tiles = self_tiles; a.kv_tiles = kv_tiles;
+  a.n_self_wg = n_self_tiles * (Hq / Hkv);
   a.sel = sel; a.R = R; a.filtered = filtered; a.E = E;
   a.tile_off = tile_off; a.row_off = row_off; a.counts = counts; a.rows = rows;
   a.delta = delta; a.part_dq = (uint16_t*)part_dq; a.kv_splits = kv_splits;

@@ -44,6 +44,7 @@ struct FwdArgs {
   float scale_log2;
   const int* cu_chunk;
   const int* self_tiles;
+  int n_self_wg;        // self workgroups: entries of self_tiles x G
   const int* sel;
   int R;
   const int* filtered;
@@ -108,18 +109,24 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void fwd_kernel(FwdArgs 
       h[qb] = sh % a.Hq;
     }
   } else {
-    // grid (q head within the kv group, tile, kv head): the G heads that
-    // share a kv head's K/V run next to each other, then the next tile of the
-    // same kv head (tiles listed largest first)
-    const int c = a.self_tiles[2 * blockIdx.y], row0 = a.self_tiles[2 * blockIdx.y + 1];
-    kh = blockIdx.z;
+    // 1-D grid over (tile, q head within the kv group), tiles in the
+    // host's order of 8 XCD runs: workgroup L runs on XCD L % 8 and takes
+    // entry xcd_contiguous(L) / G, so each run's tiles share that XCD's L2.
+    // Entries are (chunk, first row, kv head); chunk -1 pads a run.
+    const int t = xcd_contiguous(blockIdx.x, a.n_self_wg);
+    if (t < 0) return;
+    const int e = t / a.G, g = t - e * a.G;
+    const int c = a.self_tiles[3 * e];
+    if (c < 0) return;
+    const int row0 = a.self_tiles[3 * e + 1];
+    kh = a.self_tiles[3 * e + 2];
     k_lo = a.cu_chunk[c];
     const int c_end = a.cu_chunk[c + 1];
     k_hi = min(c_end, k_lo + row0 + 128 * QB);
     s_wave0 = k_lo + row0 + wave * (32 * QB);
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-      h[qb] = blockIdx.z * a.G + blockIdx.x;
+      h[qb] = kh * a.G + g;
       s[qb] = s_wave0 + qb * 32 + qi;
       valid[qb] = s[qb] < c_end;
       if (!valid[qb]) s[qb] = k_hi - 1;
@@ -411,7 +418,7 @@ int launch_fwd(const FwdArgs& a, int n_self_tiles, int max_remote_tiles, hipStre
     if (rc) return rc;
   }
   if (n_self_tiles > 0) {
-    hipLaunchKernelGGL((fwd_kernel<DT, DP, false, attn_qb<DP>()>), dim3(a.G, n_self_tiles, a.Hkv), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((fwd_kernel<DT, DP, false, attn_qb<DP>()>), dim3((unsigned)(((int64_t)n_self_tiles * a.G + 7) / 8 * 8)), dim3(256), 0, st, a);
     return moba_launch_status("prefill_fwd(self)");
   }
   return MOBA_OK;
@@ -446,12 +453,12 @@ extern "C" int moba_hip_prefill_fwd(const void* q, const void* k, const void* v,
   if (D < 8 || D > 256 || D % 8) { moba_set_error("prefill_fwd: head_dim must be a multiple of 8 in [8,256]"); return MOBA_ERR_ARG; }
   if (Hq < 1 || Hkv < 1 || Hq % Hkv) { moba_set_error("prefill_fwd: Hq must be a positive multiple of Hkv"); return MOBA_ERR_ARG; }
   if (R < 0 || R > 8) { moba_set_error("prefill_fwd: remote count must be in [0,8]"); return MOBA_ERR_ARG; }
-  if (Hq > 65535 || n_self_tiles > 65535) { moba_set_error("prefill_fwd: too many heads or self tiles"); return MOBA_ERR_ARG; }
+  if (Hq > 65535 || (int64_t)n_self_tiles * (Hq / Hkv) > (1 << 30)) { moba_set_error("prefill_fwd: too many heads or self tiles"); return MOBA_ERR_ARG; }
   FwdArgs a;
   a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v;
   a.T = T; a.Hq = Hq; a.Hkv = Hkv; a.D = D; a.G = Hq / Hkv;
   a.scale_log2 = scale * kLog2e;
-  a.cu_chunk = cu_chunk; a.self_tiles = self_tiles;
+  a.cu_chunk = cu_chunk; a.self_tiles = self_tiles; a.n_self_wg = n_self_tiles * (Hq / Hkv);
   a.sel = sel; a.R = R; a.filtered = filtered; a.E = E;
   a.tile_off = tile_off; a.row_off = row_off; a.counts = counts; a.rows = rows;
   a.part_o = (uint16_t*)part_o; a.part_ml = part_ml;

@@ -17,6 +17,7 @@ struct BwdArgs {
   float scale, scale_log2;
   const int* cu_chunk;
   const int* self_tiles;
+  int n_self_wg;        // self workgroups: entries of self_tiles x G
   const int* kv_tiles;
   const int* sel;
   int R;

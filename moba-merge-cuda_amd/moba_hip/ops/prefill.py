@@ -65,11 +65,7 @@ class PrefillPlan:
         first = []
         for c, b in enumerate(chunk_batch):
             first.append(c if c == 0 or chunk_batch[c - 1] != b else first[-1])
-        tiles = []
-        for c in range(len(att_chunk) - 1):
-            length = att_chunk[c + 1] - att_chunk[c]
-            tiles.extend((c, r0) for r0 in range(0, length, BLOCK_ROWS))
-        tiles.sort(key=lambda x: -x[1])  # most keys first
+        tiles = self._self_tile_order(att_chunk, hkv, BLOCK_ROWS)
         self.n_self_tiles = len(tiles)
         self.num_experts = self.num_filtered * hkv
         max_tiles = 0
@@ -92,7 +88,7 @@ class PrefillPlan:
         parts = OrderedDict(
             att_chunk=att_chunk, cu_chunk=cu_chunk, chunk_batch=chunk_batch, first_chunk=first,
             cu_seqlens=list(cu), filtered=filtered or [0], chunk_start=self.chunk_start or [0],
-            self_tiles=[x for t in tiles for x in t] or [0, 0], kv_tiles=kv_flat or [-1, 0, -1, 0])
+            self_tiles=[x for t in tiles for x in t] or [-1, 0, 0], kv_tiles=kv_flat or [-1, 0, -1, 0])
         flat, self._views = [], {}
         for name, vals in parts.items():
             self._views[name] = (len(flat), len(vals))
@@ -100,6 +96,48 @@ class PrefillPlan:
         self.meta = torch.tensor(flat, dtype=torch.int32).to(device, non_blocking=False)
 
     N_XCD = 8  # workgroup L of a 1-D grid runs on XCD L % 8
+
+    @classmethod
+    def _self_tile_order(cls, att_chunk, hkv, rows):
+        """Causal (self) work list: (chunk, first row, kv head) tiles of
+        `rows` query rows; a tile attends min(first row + rows, length) keys.
+
+        The tiles, listed kv head by kv head and chunk by chunk, are cut into
+        8 contiguous runs of near-equal work, one per XCD, so the tiles that
+        read one (chunk, kv head)'s keys share an L2.  In each run the tiles
+        with more than a quarter of the largest tile's keys keep that order
+        (largest first within a group); the smaller ones follow, largest
+        first, and fill the run's tail.  Runs are padded with empty tiles
+        (chunk -1) to a common length and concatenated: the kernels map
+        workgroup L to run L % 8 (xcd_contiguous).
+        """
+        items = []
+        for kh in range(hkv):
+            for c in range(len(att_chunk) - 1):
+                length = att_chunk[c + 1] - att_chunk[c]
+                for r0 in sorted(range(0, length, rows), reverse=True):
+                    items.append((min(r0 + rows, length), c, r0, kh))
+        if not items:
+            return []
+        total = sum(it[0] for it in items)
+        runs = [[] for _ in range(cls.N_XCD)]
+        acc = 0
+        for it in items:
+            # the run this tile's midpoint falls in
+            x = min(cls.N_XCD - 1, (2 * acc + it[0]) * cls.N_XCD // (2 * total))
+            runs[x].append(it)
+            acc += it[0]
+        big = max(it[0] for it in items)
+        out = []
+        n = 0
+        for x in range(cls.N_XCD):
+            head = [it for it in runs[x] if 4 * it[0] > big]
+            tail = sorted((it for it in runs[x] if 4 * it[0] <= big), key=lambda it: -it[0])
+            runs[x] = [it[1:] for it in head + tail]
+            n = max(n, len(runs[x]))
+        for x in range(cls.N_XCD):
+            out.extend(runs[x] + [(-1, 0, 0)] * (n - len(runs[x])))
+        return out
 
     def _kv_tile_order(self, att_chunk, fidx, cu, chunk_batch, cu_chunk):
         """dK/dV work list: (chunk, first key, filtered index or -1, kv head).
