@@ -132,3 +132,37 @@ def test_row_split_workspace_size():
     assert f(256, 4, 64) == -(-(16 * 1024 + 8 * 256) // 256) * 256 + 1024 * 2 * 128 * 64 * 4
     assert f(3, 2, 128) == 256 + 6 * 2 * 128 * 128 * 4
     assert f(256, 1, 64) == 0 and f(0, 4, 64) == 0 and f(8, 17, 64) == 0
+
+
+@pytest.mark.parametrize("att_chunk,hkv,rows", [
+    ([i * 4096 for i in range(9)], 32, 128),      # cfg3: 8 chunks x 32 kv heads
+    ([0, 2048, 4096, 6144, 8192], 2, 128),
+    ([0, 300, 4396], 1, 128),                     # ragged, fewer tiles than XCDs per run
+    ([0, 1, 3, 70], 3, 64),
+])
+def test_self_tile_order_is_a_partition_in_xcd_runs(att_chunk, hkv, rows):
+    """The causal work list holds every (chunk, first row, kv head) tile
+    once, in 8 equal-length runs whose attended keys differ by at most two of
+    the largest tiles, each run's tiles above a quarter of the largest first."""
+    from moba_hip.ops.prefill import PrefillPlan
+    order = PrefillPlan._self_tile_order(att_chunk, hkv, rows)
+    assert len(order) % 8 == 0
+    want = {(c, r0, kh) for kh in range(hkv) for c in range(len(att_chunk) - 1)
+            for r0 in range(0, att_chunk[c + 1] - att_chunk[c], rows)}
+    got = [t for t in order if t[0] >= 0]
+    assert len(got) == len(want) and set(got) == want
+    n = len(order) // 8
+
+    def keys(t):
+        return min(t[1] + rows, att_chunk[t[0] + 1] - att_chunk[t[0]])
+    big = max(keys(t) for t in got)
+    loads = []
+    for x in range(8):
+        run = [t for t in order[x * n:(x + 1) * n] if t[0] >= 0]
+        assert all(t[0] < 0 for t in order[x * n + len(run):(x + 1) * n])  # padding last
+        loads.append(sum(keys(t) for t in run))
+        small = [4 * keys(t) <= big for t in run]
+        assert small == sorted(small)                 # small tiles after the others
+        tail = [keys(t) for t, s in zip(run, small) if s]
+        assert tail == sorted(tail, reverse=True)
+    assert max(loads) - min(loads) <= 2 * big
