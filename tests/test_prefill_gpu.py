@@ -165,7 +165,7 @@ def test_skewed_routes_row_split(cuda_device, dim):
 
 
 def test_cfg1_mha_forward_backward(cuda_device):
-    """BASELINE cfg1 at its full size: MHA, T=4096, 8 heads, D=64, chunk 512,
+    """cfg1 at its full size: MHA, T=4096, 8 heads, D=64, chunk 512,
     topk 3, bf16 copies of seeded N(0,1) fp32 Q/K/V.  Block selection is
     bit-exact against the canonical oracle; output, LSE and all gradients are
     within the unscaled north-star bounds of the FP64 fixed-route oracle on the
