@@ -232,3 +232,46 @@ def test_cu_seqlens_in_place_write_is_seen(cuda_device):
     cu[1] = 0
     with pytest.raises(ValueError, match="strictly increase"):
         moba_hip.run_impl("opt_hip", q, k, v, cu, 320, cfg)
+
+
+@pytest.mark.parametrize("hq,hkv,dim,lens,dtype", [
+    (28, 4, 128, (1537, 511), torch.bfloat16),
+    (16, 2, 128, (2048,), torch.float16),
+    (16, 1, 80, (3073, 1023), torch.float16),
+    (32, 8, 128, (8192,), torch.bfloat16),
+])
+def test_long_prefill_against_repeat(cuda_device, hq, hkv, dim, lens, dtype):
+    """GQA against the same call with K/V repeated to Hq heads (the MHA
+    kernels and their schedules): outputs and dQ agree, and each kv head's
+    dK/dV equals the sum over its group of the repeated heads' gradients.
+    Shapes and bounds of tests/test_grouped_scale.py:10-25 in the reference
+    (its `compare`, tests/test_grouped_attention.py:23-33)."""
+    import moba_hip
+    q, k, v, cu, ml, g = prefill_inputs(hq, hkv, dim, lens, dtype, seed=77)
+    cfg = {"chunk_size": 128 if sum(lens) < 8192 else 512, "topk": 4}
+    G = hq // hkv
+
+    def run(kk, vv):
+        qr, kr, vr = (x.detach().requires_grad_(True) for x in (q, kk, vv))
+        out = moba_hip.run_impl("opt_hip", qr, kr, vr, cu, ml, cfg)
+        return (out,) + torch.autograd.grad(out, (qr, kr, vr), grad_outputs=g)
+
+    o_g, dq_g, dk_g, dv_g = run(k, v)
+    o_r, dq_r, dk_r, dv_r = run(k.repeat_interleave(G, 1), v.repeat_interleave(G, 1))
+    T = q.shape[0]
+    dk_r = dk_r.float().view(T, hkv, G, dim).sum(2)
+    dv_r = dv_r.float().view(T, hkv, G, dim).sum(2)
+
+    def compare(a, b):
+        af, bf = a.float(), b.float()
+        assert torch.isfinite(af).all()
+        rel = (torch.linalg.vector_norm(af - bf) / torch.linalg.vector_norm(bf).clamp_min(1e-8)).item()
+        if dtype == torch.bfloat16:
+            torch.testing.assert_close(af, bf, atol=0.04, rtol=0.03)
+            assert rel < 0.01
+        else:
+            torch.testing.assert_close(af, bf, atol=0.003, rtol=0.003)
+            assert rel < 0.002
+
+    for a, b in ((o_g, o_r), (dq_g, dq_r), (dk_g, dk_r), (dv_g, dv_r)):
+        compare(a, b)
