@@ -75,13 +75,16 @@ def _check_tensor(name, t, q):
 # the stream (about 0.2 ms of idle GPU per prefill step); the same tensor,
 # not modified in place since (torch bumps its version counter on every
 # in-place write), reuses its copy.  Writes that bypass torch (raw pointers)
-# are not seen: pass a new tensor after such a write.
+# are not seen: pass a new tensor after such a write.  Inference-mode tensors
+# have no version counter and are read on every call.
 _CU_HOST = OrderedDict()
 _CU_HOST_MAX = 16
 _CU_LOCK = threading.Lock()
 
 
 def _host_cu(cu_t):
+    if cu_t.is_inference():
+        return cu_t.tolist()
     key = id(cu_t)
     with _CU_LOCK:
         hit = _CU_HOST.get(key)

@@ -166,3 +166,21 @@ def test_self_tile_order_is_a_partition_in_xcd_runs(att_chunk, hkv, rows):
         tail = [keys(t) for t, s in zip(run, small) if s]
         assert tail == sorted(tail, reverse=True)
     assert max(loads) - min(loads) <= 2 * big
+
+
+def test_cu_seqlens_host_copy_follows_writes():
+    """The host copy of cu_seqlens is reused only while the tensor is
+    unchanged; inference-mode tensors (no version counter) are re-read."""
+    from moba_hip.baseline_adapter import _host_cu
+    cu = torch.tensor([0, 5, 9], dtype=torch.int32)
+    assert _host_cu(cu) == [0, 5, 9]
+    cu[1] = 4
+    assert _host_cu(cu) == [0, 4, 9]
+    cu[1:].add_(1)                       # a write through a view
+    assert _host_cu(cu) == [0, 5, 10]
+    with torch.inference_mode():
+        ci = torch.tensor([0, 3], dtype=torch.int32)
+        assert _host_cu(ci) == [0, 3]
+        ci[1] = 2
+        assert _host_cu(ci) == [0, 2]
+    assert _host_cu(ci) == [0, 2]

@@ -275,3 +275,21 @@ def test_long_prefill_against_repeat(cuda_device, hq, hkv, dim, lens, dtype):
 
     for a, b in ((o_g, o_r), (dq_g, dq_r), (dk_g, dk_r), (dv_g, dv_r)):
         compare(a, b)
+
+
+def test_inference_mode_forward(cuda_device):
+    """A forward under torch.inference_mode (inference tensors, cu_seqlens
+    included) equals the differentiable forward bit for bit."""
+    import moba_hip
+    q, k, v, cu, ml, _ = prefill_inputs(8, 2, 64, (300, 77), torch.bfloat16, seed=5)
+    cfg = {"chunk_size": 32, "topk": 3}
+    ref = moba_hip.run_impl("opt_hip", q, k, v, cu, ml, cfg)
+    with torch.inference_mode():
+        qi, ki, vi, ci = (x.clone() for x in (q, k, v, cu))
+        out = moba_hip.run_impl("opt_hip", qi, ki, vi, ci, ml, cfg)
+        assert torch.equal(out, ref)
+        ci[1] = 200   # a new split of the same tokens is read, not a stale copy
+        out2 = moba_hip.run_impl("opt_hip", qi, ki, vi, ci, 200, cfg)
+    fresh = moba_hip.run_impl("opt_hip", q, k, v, torch.tensor([0, 200, 377], dtype=torch.int32,
+                                                                device=q.device), 200, cfg)
+    assert torch.equal(out2, fresh)
