@@ -226,3 +226,30 @@ def test_prepared_route_ties_pick_lowest_chunks(cuda_device, dtype):
                 cur = int(sel[row, 0, 0])
                 want = list(range(min(3, cur)))
                 assert sel[row, :, 1:1 + len(want)].tolist() == [want] * 12
+
+
+@pytest.mark.parametrize("graph", [False, True])
+def test_decode_under_inference_mode(cuda_device, graph):
+    """A cache built, filled and stepped entirely under torch.inference_mode
+    gives the same outputs, routes and lengths as the same calls without it."""
+    def run(inference):
+        with torch.inference_mode(inference):
+            cache = _paged()(2, 64, 2, 64, page_size=5, chunk_size=8)
+            k, v = rand((30, 2, 64), torch.bfloat16, 601), rand((30, 2, 64), torch.bfloat16, 602)
+            cache.append(k, v, sequence_ids=[1, 0], cu_seqlens=[0, 17, 30])
+            outs = [cache.attend(rand((2, 6, 64), torch.bfloat16, 603), sequence_ids=[1, 0],
+                                 topk=3).output.clone()]
+            with cache.prepare_decode([1, 0], 6, topk=3) as plan:
+                if graph:
+                    plan.capture("step")
+                for step in range(4):
+                    r = plan.step(rand((2, 6, 64), torch.bfloat16, 610 + step),
+                                  rand((2, 2, 64), torch.bfloat16, 620 + step),
+                                  rand((2, 2, 64), torch.bfloat16, 630 + step), use_graph=graph)
+                    outs += [r.output.clone(), r.selected_blocks.clone()]
+            return outs, cache.lengths
+
+    (a, la), (b, lb) = run(False), run(True)
+    assert la == lb
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
