@@ -293,3 +293,26 @@ def test_inference_mode_forward(cuda_device):
     fresh = moba_hip.run_impl("opt_hip", q, k, v, torch.tensor([0, 200, 377], dtype=torch.int32,
                                                                 device=q.device), 200, cfg)
     assert torch.equal(out2, fresh)
+
+
+def test_strided_inputs_match_contiguous(cuda_device):
+    """q/k/v that are head slices of wider tensors (last dim contiguous, rows
+    strided) and a transposed-layout upstream gradient give the results of
+    their contiguous copies bit for bit, gradients in the input layout."""
+    import moba_hip
+    q, k, v, cu, ml, g = prefill_inputs(6, 2, 64, (150, 90), torch.bfloat16, seed=9)
+    cfg = {"chunk_size": 32, "topk": 3}
+
+    def run(qq, kk, vv, gg):
+        qr, kr, vr = (x.detach().requires_grad_(True) for x in (qq, kk, vv))
+        out = moba_hip.run_impl("opt_hip", qr, kr, vr, cu, ml, cfg)
+        return (out,) + torch.autograd.grad(out, (qr, kr, vr), grad_outputs=gg)
+
+    ref = run(q, k, v, g)
+    wide = [torch.cat([x, torch.zeros_like(x)], 1)[:, :x.shape[1]] for x in (q, k, v)]
+    assert not any(x.is_contiguous() for x in wide)
+    gt = g.transpose(0, 1).contiguous().transpose(0, 1)   # [T,H,D] view of a [H,T,D] buffer
+    got = run(*wide, gt)
+    for a, b in zip(got, ref):
+        assert torch.equal(a, b)
+    assert got[1].shape == q.shape and got[2].shape == k.shape
