@@ -316,3 +316,30 @@ def test_strided_inputs_match_contiguous(cuda_device):
     for a, b in zip(got, ref):
         assert torch.equal(a, b)
     assert got[1].shape == q.shape and got[2].shape == k.shape
+
+
+def test_side_stream_orders_after_its_producers(cuda_device):
+    """Forward and backward issued on a side stream run on that stream: with
+    the inputs produced there behind a busy-wait kernel, the results equal
+    the default-stream ones (a launch on another stream would read the
+    inputs before they are written)."""
+    import moba_hip
+    q, k, v, cu, ml, g = prefill_inputs(4, 2, 64, (200, 60), torch.bfloat16, seed=13)
+    cfg = {"chunk_size": 32, "topk": 3}
+
+    def run(qq, kk, vv):
+        qr, kr, vr = (x.detach().requires_grad_(True) for x in (qq, kk, vv))
+        out = moba_hip.run_impl("opt_hip", qr, kr, vr, cu, ml, cfg)
+        return (out,) + torch.autograd.grad(out, (qr, kr, vr), grad_outputs=g)
+
+    ref = run(q, k, v)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        torch.cuda._sleep(20_000_000)   # a few ms of device time before the inputs exist
+        q2, k2, v2 = (x * 1 for x in (q, k, v))
+        got = run(q2, k2, v2)
+    torch.cuda.synchronize()
+    for a, b in zip(got, ref):
+        assert torch.equal(a, b)
