@@ -8,6 +8,7 @@ by tensor object (lru_cache, diagnostic.py:30).
 """
 from __future__ import annotations
 
+import threading
 from collections import OrderedDict
 
 import torch
@@ -180,18 +181,24 @@ class PrefillPlan:
 
 
 _PLANS: "OrderedDict[tuple, PrefillPlan]" = OrderedDict()
+_PLANS_LOCK = threading.Lock()
 
 
 def get_plan(cu, chunk, hq, hkv, head_dim, topk, device, fallback=False):
+    """The cached plan of a shape (16 most recent; safe to call from several
+    threads: a plan is immutable once built)."""
     key = (tuple(cu), chunk, hq, hkv, head_dim, topk, str(device), fallback)
-    plan = _PLANS.get(key)
-    if plan is None:
-        plan = PrefillPlan(cu, chunk, hq, hkv, head_dim, topk, device, fallback)
+    with _PLANS_LOCK:
+        plan = _PLANS.get(key)
+        if plan is not None:
+            _PLANS.move_to_end(key)
+            return plan
+    plan = PrefillPlan(cu, chunk, hq, hkv, head_dim, topk, device, fallback)
+    with _PLANS_LOCK:
         _PLANS[key] = plan
-        if len(_PLANS) > 16:
-            _PLANS.popitem(last=False)
-    else:
         _PLANS.move_to_end(key)
+        while len(_PLANS) > 16:
+            _PLANS.popitem(last=False)
     return plan
 
 

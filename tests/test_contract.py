@@ -184,3 +184,27 @@ def test_cu_seqlens_host_copy_follows_writes():
         ci[1] = 2
         assert _host_cu(ci) == [0, 2]
     assert _host_cu(ci) == [0, 2]
+
+
+def test_plan_cache_is_thread_safe():
+    """Concurrent plan lookups over more shapes than the cache holds (so
+    entries are evicted while others are read) neither raise nor mix plans."""
+    import threading
+    from moba_hip.ops import prefill as P
+    errors = []
+
+    def worker(seed):
+        try:
+            for i in range(60):
+                n = 64 + 16 * ((seed * 7 + i) % 24)
+                plan = P.get_plan([0, n], 16, 4, 2, 64, 3, "cpu")
+                assert plan.cu == [0, n]
+        except Exception as e:  # noqa: BLE001 - reported below
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=worker, args=(s,)) for s in range(8)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors[:3]
