@@ -571,11 +571,12 @@ __global__ __launch_bounds__(64 * FW) void fused_kernel(FusedArgs a) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   };
   {
-    // wave w takes blocks b0 + w, b0 + w + kFW, ...: 12-wave form one
-    // register buffer, 8-wave form two (ping-pong: block b + kFW loads while
-    // block b computes)
+    // wave w takes blocks b0 + w, b0 + w + kFW, ...: 12-wave form and head
+    // dims above 128 one register buffer, 8-wave form two (ping-pong: block
+    // b + kFW loads while block b computes).  Two 256-wide buffers need more
+    // than the 256 registers of a 2-wave-per-SIMD launch (about 700 spilled).
     int b = b0 + w;
-    if constexpr (FW > kFwNarrow) {
+    if constexpr (FW > kFwNarrow || DP > 128) {
       // one register buffer: load, then compute, block after block
       for (; b < b1; b += kFW) {
         u16x8_t kA[2][NKS], vA[VLD];
