@@ -160,18 +160,23 @@ __global__ __launch_bounds__(64) void means_kernel(const uint16_t* __restrict__ 
 }
 
 // ------------------------------------------------------------------- route
-// One workgroup (4 waves) per (query row, kv head).  Wave w scores the heads
-// g = w, w+4, ... of the group: lane j takes chunks j, j+64, ... (fp32 fma
+// One workgroup (up to 8 waves) per (query row, kv head, block of 16 q heads).
+// Wave w scores the heads g = w, w+nw, ... of the block: lane j takes chunks
+// j, j+64, ... (fp32 fma
 // chain over d, the canonical gate order) against the cache-dtype means; the
 // stable top-R is R rounds of a wave argmax, each round taking the best
 // candidate strictly after the previous pick in (score desc, chunk asc) order.
-// Thread 0 then writes the work list of every 16-head block.
+// The workgroup then writes its block's work list.
 struct WorkItem {
   int chunk, mask, slots_lo, slots_hi;  // slots: 4 bits per head of the block
 };
 
+// Waves per route workgroup: at most 8, or 4 above 128 dims, where the q
+// row and a means row held in registers take 256 of them.
+template <int DP> constexpr int route_max_waves() { return DP > 128 ? 4 : 8; }
+
 template <int DT, int DP, bool VEC>
-__global__ __launch_bounds__(1024) void route_kernel(const uint16_t* __restrict__ q, int Hq, int Hkv,
+__global__ __launch_bounds__(64 * route_max_waves<DP>()) void route_kernel(const uint16_t* __restrict__ q, int Hq, int Hkv,
                                                      int D, const uint16_t* __restrict__ means,
                                                      int max_chunks, const int* __restrict__ seq,
                                                      const int* __restrict__ pos, int C, int width,
@@ -186,14 +191,16 @@ __global__ __launch_bounds__(1024) void route_kernel(const uint16_t* __restrict_
   __shared__ int n_s;
   const int G = Hq / Hkv, NHB = (G + 15) / 16;
   const int nw = blockDim.x >> 6;
-  const int qrow = blockIdx.x / Hkv, kh = blockIdx.x % Hkv;
+  const int hb = blockIdx.x % NHB, rk = blockIdx.x / NHB;  // rk = qrow * Hkv + kh
+  const int qrow = rk / Hkv, kh = rk % Hkv;
+  const int g_lo = hb * 16, g_hi = min(G, g_lo + 16);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int sid = seq[qrow], p = pos[qrow];
   const int legal = min(p / C, width);  // chunks c with (c+1)*C <= p
   float* sc = sc_lds + w * width;
-  for (int g0 = 0; g0 < G; g0 += nw) {
+  for (int g0 = g_lo; g0 < g_hi; g0 += nw) {
     const int g = g0 + w;
-    if (g < G) {
+    if (g < g_hi) {
       const int h = kh * G + g;
       const int64_t idx = (int64_t)qrow * Hq + h;
       const uint16_t* qr = q + idx * D;
@@ -270,8 +277,8 @@ __global__ __launch_bounds__(1024) void route_kernel(const uint16_t* __restrict_
   // chose each chunk and their slot indices.  Built in parallel: entry e finds
   // its first occurrence by comparison, ranks come from a ballot prefix count.
   const int S = R + 1;
-  for (int hb = 0; hb < NHB; ++hb) {
-    const int g_lo = hb * 16, ng = min(16, G - g_lo), E = ng * S;
+  {
+    const int ng = g_hi - g_lo, E = ng * S;
     for (int e = threadIdx.x; e < E; e += blockDim.x) {
       const int c = sel_s[g_lo * S + e];
       int first = -1;
@@ -307,9 +314,9 @@ __global__ __launch_bounds__(1024) void route_kernel(const uint16_t* __restrict_
     }
     __syncthreads();
     const int n = n_s;
-    WorkItem* it = items + ((int64_t)blockIdx.x * NHB + hb) * max_items;
+    WorkItem* it = items + ((int64_t)rk * NHB + hb) * max_items;
     for (int x = threadIdx.x; x < n; x += blockDim.x) it[x] = it_s[x];
-    if (threadIdx.x == 0) item_counts[blockIdx.x * NHB + hb] = n;
+    if (threadIdx.x == 0) item_counts[rk * NHB + hb] = n;
     __syncthreads();
   }
 }
@@ -335,14 +342,20 @@ struct AttnArgs {
   float* lse;
 };
 
+// Waves per attention workgroup: 8, or 4 above 128 dims, where the K/V
+// register blocks and O accumulators of a wave need more than the 256
+// registers of two waves per SIMD (8 waves spilled 145-655 registers).
+template <int DP> constexpr int attn_waves() { return DP > 128 ? 4 : kWaves; }
+
 template <int DT, int DP, bool VEC>
-__global__ __launch_bounds__(512) void attn_kernel(AttnArgs a) {
+__global__ __launch_bounds__(64 * attn_waves<DP>()) void attn_kernel(AttnArgs a) {
+  constexpr int NW = attn_waves<DP>();
   constexpr int NKS = DP / 32;  // 32-d k-steps of S^T
   constexpr int NDB = DP / 16;  // 16-d blocks of O^T
   constexpr int VS = DP + 8;
   constexpr int STAGE = 32 * VS;  // per-wave V tile (elements)
-  constexpr int STAGE_BYTES = kWaves * STAGE * 2;
-  constexpr int MERGE_BYTES = kWaves * (16 * DP + 32) * 4;
+  constexpr int STAGE_BYTES = NW * STAGE * 2;
+  constexpr int MERGE_BYTES = NW * (16 * DP + 32) * 4;
   __shared__ __attribute__((aligned(16))) unsigned char lds[STAGE_BYTES > MERGE_BYTES ? STAGE_BYTES : MERGE_BYTES];
   uint16_t* Vs = reinterpret_cast<uint16_t*>(lds) + (threadIdx.x >> 6) * STAGE;
 
@@ -394,10 +407,9 @@ __global__ __launch_bounds__(512) void attn_kernel(AttnArgs a) {
   for (int db = 0; db < NDB; ++db) oacc[db] = (f32x4v){0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, lsum = 0.0f;
 
-  // wave w takes the 32-token steps w, w + 8, ... of the chunk; the K rows and
+  // wave w takes the 32-token steps w, w + NW, ... of the chunk; the K rows and
   // V rows of the next step are loaded into registers while this one computes
   constexpr int VLD = 32 * (DP / 8) / 64;  // 16-byte V chunks per lane per step
-  constexpr bool PREFETCH = DP <= 128;
   // Page of token t0 + r (0 <= r < 32) from one division per step: pages of at
   // least 32 tokens hold the step in at most two pages.
   auto page_of = [&](int t0, int pg0, int off0, int r) -> int {
@@ -511,32 +523,23 @@ __global__ __launch_bounds__(512) void attn_kernel(AttnArgs a) {
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   };
-  constexpr int kStride = 32 * kWaves;
+  constexpr int kStride = 32 * NW;
   int tt = t_begin + 32 * w;
   if (tt < t_end) {
     u16x8_t kr[2][NKS], vr[VLD];
     load(tt, kr, vr);
-    if constexpr (PREFETCH) {
-      for (; tt + kStride < t_end; tt += kStride) {
-        u16x8_t kn[2][NKS], vn[VLD];
-        load(tt + kStride, kn, vn);
-        compute(tt, kr, vr);
-#pragma unroll
-        for (int half = 0; half < 2; ++half)
-#pragma unroll
-          for (int ks = 0; ks < NKS; ++ks) kr[half][ks] = kn[half][ks];
-#pragma unroll
-        for (int x = 0; x < VLD; ++x) vr[x] = vn[x];
-      }
+    for (; tt + kStride < t_end; tt += kStride) {
+      u16x8_t kn[2][NKS], vn[VLD];
+      load(tt + kStride, kn, vn);
       compute(tt, kr, vr);
-    } else {
-      for (;;) {
-        compute(tt, kr, vr);
-        tt += kStride;
-        if (tt >= t_end) break;
-        load(tt, kr, vr);
-      }
+#pragma unroll
+      for (int half = 0; half < 2; ++half)
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) kr[half][ks] = kn[half][ks];
+#pragma unroll
+      for (int x = 0; x < VLD; ++x) vr[x] = vn[x];
     }
+    compute(tt, kr, vr);
   }
   lsum += __shfl_xor(lsum, 16, 64);
   lsum += __shfl_xor(lsum, 32, 64);
@@ -553,16 +556,16 @@ __global__ __launch_bounds__(512) void attn_kernel(AttnArgs a) {
     for (int e = 0; e < 4; ++e) wo[c16 * DP + db * 16 + 4 * g4 + e] = oacc[db][e];
   if (g4 == 0) { wo[16 * DP + c16] = m_run; wo[16 * DP + 16 + c16] = lsum; }
   __syncthreads();
-  for (int x = tid; x < 16 * DP; x += 512) {
+  for (int x = tid; x < 16 * DP; x += 64 * NW) {
     const int hh = x / DP, d = x % DP;
     if (!((mask >> hh) & 1) || d >= D) continue;
     float M = -INFINITY;
-    for (int ww = 0; ww < kWaves; ++ww) {
+    for (int ww = 0; ww < NW; ++ww) {
       const float* o = mrg + ww * (16 * DP + 32);
       if (o[16 * DP + 16 + hh] > 0.0f) M = fmaxf(M, o[16 * DP + hh]);
     }
     float z = 0.0f, acc = 0.0f;
-    for (int ww = 0; ww < kWaves; ++ww) {
+    for (int ww = 0; ww < NW; ++ww) {
       const float* o = mrg + ww * (16 * DP + 32);
       const float l = o[16 * DP + 16 + hh];
       if (l > 0.0f) {
@@ -715,9 +718,9 @@ int launch_attn(const AttnArgs& a, int n_items, hipStream_t st) {
   if (ny < 1) ny = 1;
   dim3 grid((unsigned)rows, (unsigned)ny);
   if (a.D % 8 == 0)
-    hipLaunchKernelGGL((attn_kernel<DT, DP, true>), grid, dim3(64 * kWaves), 0, st, a);
+    hipLaunchKernelGGL((attn_kernel<DT, DP, true>), grid, dim3(64 * attn_waves<DP>()), 0, st, a);
   else
-    hipLaunchKernelGGL((attn_kernel<DT, DP, false>), grid, dim3(64 * kWaves), 0, st, a);
+    hipLaunchKernelGGL((attn_kernel<DT, DP, false>), grid, dim3(64 * attn_waves<DP>()), 0, st, a);
   hipLaunchKernelGGL(combine_kernel<DT>, dim3((unsigned)(a.Nq * a.Hq)), dim3(64), 0, st, a);
   return moba_launch_status("paged_attention");
 }
@@ -790,12 +793,17 @@ extern "C" int moba_hip_decode_route(const void* q, int dtype, int Nq, int Hq, i
   if (Nq <= 0) return MOBA_OK;
   hipStream_t st = (hipStream_t)stream;
   const int G = Hq / Hkv;
-  int nw = G < 16 ? G : 16;  // one wave per q head, bounded by the score buffers' LDS
+  // one wave per q head of a 16-head block, at most route_max_waves (the
+  // kernel's register budget), bounded by the score buffers' LDS
+  const int wmax = D % 8 != 0 ? route_max_waves<8>() : D <= 128 ? route_max_waves<128>()
+                                                                : route_max_waves<256>();
+  int nw = G < wmax ? G : wmax;
   const int wb = (width > 0 ? width : 1) * (int)sizeof(float);
   while (nw > 1 && nw * wb > 96 * 1024) --nw;
   const size_t lds = (size_t)nw * wb;
   const int max_items = G * (R + 1);
-  dim3 grid((unsigned)(Nq * Hkv)), block(64 * nw);
+  const int NHB = (G + 15) / 16;
+  dim3 grid((unsigned)(Nq * Hkv * NHB)), block(64 * nw);
 #define MOBA_ROUTE(DT_, DP_, VEC_)                                                              \
   hipLaunchKernelGGL((route_kernel<DT_, DP_, VEC_>), grid, block, lds, st, (const uint16_t*)q,   \
                      Hq, Hkv, D, (const uint16_t*)means, max_chunks, q_seq, q_pos, chunk, width, \

@@ -310,3 +310,19 @@ def test_unmapped_page_is_never_written(cuda_device):
     kernels.append_tokens(k, k, cache.k_cache, cache.v_cache, table, ids, pos)
     torch.cuda.synchronize()
     assert int(cache.k_cache.count_nonzero()) == 0 and int(cache.v_cache.count_nonzero()) == 0
+
+
+@pytest.mark.parametrize("dim", [136, 200, 256])
+def test_wide_groups_wide_heads(cuda_device, dim):
+    """More than 16 q heads per kv head take the multi-kernel path; above 128
+    dims its attention workgroups run 4 waves.  Attend and append-and-attend
+    against the oracle, moba and dense."""
+    Paged, _ = _caches()
+    cache = Paged(3, 200, 1, dim, page_size=9, chunk_size=16, dtype=torch.bfloat16)
+    k, v = rand((150, 1, dim), torch.bfloat16, 171), rand((150, 1, dim), torch.bfloat16, 172)
+    cache.append(k, v, sequence_ids=[0, 1, 2], cu_seqlens=[0, 61, 100, 150])
+    q = rand((3, 32, dim), torch.bfloat16, 173)
+    for mode in ("moba", "dense"):
+        check(cache, cache.attend(q, sequence_ids=[0, 1, 2], topk=3, mode=mode), q)
+    kn, vn = rand((3, 1, dim), torch.bfloat16, 174), rand((3, 1, dim), torch.bfloat16, 175)
+    check(cache, cache.append_and_attend(q, kn, vn, sequence_ids=[0, 1, 2], topk=3), q)
