@@ -16,7 +16,7 @@ def _paged():
 @pytest.mark.parametrize("graph", [False, True])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("page,chunk,dim,hq,hk", [(3, 4, 33, 15, 3), (7, 6, 64, 8, 1),
-                                                   (16, 8, 128, 8, 2)])
+                                                   (16, 8, 128, 8, 2), (5, 8, 256, 6, 2)])
 def test_prepared_steps_match_fp64(cuda_device, graph, dtype, page, chunk, dim, hq, hk):
     cache = _paged()(3, 40, hk, dim, page_size=page, chunk_size=chunk, dtype=dtype)
     k, v = rand((14, hk, dim), dtype, 501), rand((14, hk, dim), dtype, 502)
