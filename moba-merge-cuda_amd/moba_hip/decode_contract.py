@@ -75,6 +75,26 @@ def tensor(t, name, *, device, dtype, head_dim, heads=None, tokens=None, finite=
     ])
 
 
+def finite(t, name):
+    _require([(lambda: bool(torch.isfinite(t).all()), f"{name} contains NaN/Inf")])
+
+
+def tensors(specs, *, device, dtype, head_dim):
+    """`tensor` for each (t, name, kwargs) in order, raising what those calls
+    in sequence would raise first; the NaN/Inf test of all inputs reads one
+    flag (one host synchronisation instead of one per tensor)."""
+    for i, (t, name, kw) in enumerate(specs):
+        try:
+            tensor(t, name, device=device, dtype=dtype, head_dim=head_dim, finite=False, **kw)
+        except ValueError:
+            for t0, n0, _ in specs[:i]:  # an earlier input's NaN/Inf comes first
+                finite(t0, n0)
+            raise
+    if len(specs) == 1 or not bool(torch.stack([torch.isfinite(t).all() for t, _, _ in specs]).all()):
+        for t, name, _ in specs:
+            finite(t, name)
+
+
 def append_counts(token_count, ids, cu_seqlens):
     """Tokens per sequence from cu_seqlens (one token each when None)."""
     cu = tuple(range(len(ids) + 1)) if cu_seqlens is None else int_vector(cu_seqlens, "cu_seqlens")

@@ -105,9 +105,8 @@ class PagedKVCache:
              "cross-stream cache access is unsupported"),
         ])
 
-    def _check_input(self, t, name, **kw):
-        contract.tensor(t, name, device=self.device, dtype=self.dtype, head_dim=self.head_dim,
-                        **kw)
+    def _check_inputs(self, *specs):
+        contract.tensors(specs, device=self.device, dtype=self.dtype, head_dim=self.head_dim)
 
     def _no_pool_alias(self, *tensors):
         pools = (self.k_cache.untyped_storage().data_ptr(),
@@ -150,8 +149,8 @@ class PagedKVCache:
     def append(self, k, v, *, sequence_ids, cu_seqlens=None):
         with self._lock, torch.cuda.device(self.device):
             self._guard()
-            self._check_input(k, "k", heads=self.num_kv_heads)
-            self._check_input(v, "v", heads=self.num_kv_heads, tokens=k.shape[0])
+            self._check_inputs((k, "k", {"heads": self.num_kv_heads}),
+                               (v, "v", {"heads": self.num_kv_heads, "tokens": k.shape[0]}))
             self._no_pool_alias(k, v)
             ids = self._layout.validate_ids(_ints(sequence_ids, "sequence_ids"), unique=True)
             counts = contract.append_counts(k.shape[0], ids, cu_seqlens)
@@ -179,7 +178,7 @@ class PagedKVCache:
 
     # ----------------------------------------------------------------- attend
     def _positions(self, q, sequence_ids, positions):
-        self._check_input(q, "q")
+        self._check_inputs((q, "q", {}))
         _require([(lambda: q.shape[1] % self.num_kv_heads == 0, "Hq must be a multiple of Hkv")])
         ids = self._layout.validate_ids(_ints(sequence_ids, "sequence_ids"))
         _require([(lambda: len(ids) == q.shape[0], "one sequence ID per query row required")])
@@ -240,9 +239,9 @@ class PagedKVCache:
         with self._lock, torch.cuda.device(self.device):
             self._guard()
             dense = _mode(mode, topk)
-            self._check_input(k, "k", heads=self.num_kv_heads)
-            self._check_input(v, "v", heads=self.num_kv_heads, tokens=k.shape[0])
-            self._check_input(q, "q", tokens=k.shape[0])
+            self._check_inputs((k, "k", {"heads": self.num_kv_heads}),
+                               (v, "v", {"heads": self.num_kv_heads, "tokens": k.shape[0]}),
+                               (q, "q", {"tokens": k.shape[0]}))
             self._no_pool_alias(q, k, v)
             contract.query_grid(q, self.num_kv_heads)
             ids = self._layout.validate_ids(_ints(sequence_ids, "sequence_ids"), unique=True)

@@ -194,9 +194,28 @@ class PreparedDecode:
             own = {t.untyped_storage().data_ptr() for t in (self.q, self.k, self.v)}
             _require([(lambda: given.untyped_storage().data_ptr() not in own,
                        "input aliases another prepared workspace; clone first")])
-        if self.check_finite:
-            _require([(lambda: bool(torch.isfinite(given).all()), f"{name} contains NaN/Inf")])
         return given is not buffer
+
+    def _bind_all(self, specs):
+        """`_bind` for each (given, buffer, name) in order, then the NaN/Inf
+        test of all of them through one flag (one host synchronisation, not
+        one per input).  Raises what binding and testing each input in turn
+        would raise first.  Returns the (given, buffer) pairs to copy."""
+        copies = []
+        for i, (t, b, n) in enumerate(specs):
+            try:
+                if self._bind(t, b, n):
+                    copies.append((t, b))
+            except ValueError:
+                if self.check_finite:  # an earlier input's NaN/Inf comes first
+                    for t0, _, n0 in specs[:i]:
+                        contract.finite(t0, n0)
+                raise
+        if self.check_finite and (len(specs) == 1 or not bool(
+                torch.stack([torch.isfinite(t).all() for t, _, _ in specs]).all())):
+            for t, _, n in specs:
+                contract.finite(t, n)
+        return copies
 
     # ---------------------------------------------------------------- run
     def _run(self, append, use_graph, stream):
@@ -245,7 +264,7 @@ class PreparedDecode:
     def attend(self, q, *, use_graph=False):
         with self.cache._lock:
             stream = self._usable()
-            copy_q = self._bind(q, self.q, "q")
+            copy_q = bool(self._bind_all(((q, self.q, "q"),)))
             if use_graph and "attend" not in self._captured:
                 raise ValueError("capture('attend') first")
             if copy_q:
@@ -262,8 +281,7 @@ class PreparedDecode:
                 if use_graph and "step" not in self._captured:
                     raise ValueError("capture('step') first")
                 return self._result(self._run(True, use_graph, stream))
-            copies = [(t, b) for t, b, n in ((q, self.q, "q"), (k, self.k, "k"), (v, self.v, "v"))
-                      if self._bind(t, b, n)]
+            copies = self._bind_all(((q, self.q, "q"), (k, self.k, "k"), (v, self.v, "v")))
             if use_graph and "step" not in self._captured:
                 raise ValueError("capture('step') first")
             positions = self._plan_step(stream)  # refuses (ValueError) before any change

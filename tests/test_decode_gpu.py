@@ -326,3 +326,29 @@ def test_wide_groups_wide_heads(cuda_device, dim):
         check(cache, cache.attend(q, sequence_ids=[0, 1, 2], topk=3, mode=mode), q)
     kn, vn = rand((3, 1, dim), torch.bfloat16, 174), rand((3, 1, dim), torch.bfloat16, 175)
     check(cache, cache.append_and_attend(q, kn, vn, sequence_ids=[0, 1, 2], topk=3), q)
+
+
+def test_input_errors_follow_argument_order(cuda_device):
+    """Inputs are checked k, v, q, each fully before the next (the reference's
+    per-tensor order), although NaN/Inf is tested for all of them at once:
+    the first failing input's error is raised and nothing is written."""
+    Paged, _ = _caches()
+    cache = Paged(2, 32, 2, 16, page_size=4, chunk_size=8)
+    k, v = rand((5, 2, 16), torch.bfloat16, 181), rand((5, 2, 16), torch.bfloat16, 182)
+    cache.append(k, v, sequence_ids=[0], cu_seqlens=[0, 5])
+    lengths = cache.lengths
+    q, kn, vn = (rand((1, h, 16), torch.bfloat16, 183 + h) for h in (4, 2, 2))
+    nan = float("nan")
+    cases = [
+        ((q, kn * nan, vn[:, :1]), "k contains NaN/Inf"),       # before v's shape
+        ((q * nan, kn, vn * nan), "v contains NaN/Inf"),        # before q's NaN
+        ((q[:, :, :8], kn, vn * nan), "v contains NaN/Inf"),    # before q's shape
+        ((q * nan, kn, vn), "q contains NaN/Inf"),
+        ((q[:, :, :8], kn, vn), "q has an invalid shape"),
+    ]
+    for (qq, kk, vv), msg in cases:
+        with pytest.raises(ValueError, match=msg):
+            cache.append_and_attend(qq, kk, vv, sequence_ids=[0])
+    with pytest.raises(ValueError, match="k contains NaN/Inf"):
+        cache.append(kn * nan, vn[:, :1], sequence_ids=[0])
+    assert cache.lengths == lengths

@@ -253,3 +253,27 @@ def test_decode_under_inference_mode(cuda_device, graph):
     assert la == lb
     for x, y in zip(a, b):
         assert torch.equal(x, y)
+
+
+def test_step_input_errors_follow_argument_order(cuda_device):
+    """q, k, v are checked in that order, each fully before the next, with
+    the NaN/Inf test of all three through one flag; nothing changes."""
+    cache = _paged()(2, 40, 2, 16, page_size=4, chunk_size=8)
+    k, v = rand((9, 2, 16), torch.bfloat16, 701), rand((9, 2, 16), torch.bfloat16, 702)
+    cache.append(k, v, sequence_ids=[0, 1], cu_seqlens=[0, 4, 9])
+    nan = float("nan")
+    with cache.prepare_decode([0, 1], 4, topk=2) as p:
+        q, kn, vn = rand((2, 4, 16), torch.bfloat16, 703), *(rand((2, 2, 16), torch.bfloat16, s)
+                                                              for s in (704, 705))
+        lengths = cache.lengths
+        cases = [((q * nan, kn[:1], vn), "q contains NaN/Inf"),
+                 ((q, kn * nan, vn * nan), "k contains NaN/Inf"),
+                 ((q, kn, vn * nan), "v contains NaN/Inf"),
+                 ((q, kn * nan, vn[:1]), "k contains NaN/Inf"),
+                 ((q, kn, vn[:1]), "v must have fixed shape")]
+        for args, msg in cases:
+            with pytest.raises(ValueError, match=msg):
+                p.step(*args)
+        assert cache.lengths == lengths
+        r = p.step(q, kn, vn)
+        assert cache.lengths == tuple(n + 1 for n in lengths) and r.output.isfinite().all()
