@@ -55,7 +55,7 @@ def _flags(src: Path):
 
 
 def _compile(src: Path, force: bool) -> Path:
-    obj = OUT_DIR / (src.stem + ".o")
+    obj = OUT_DIR / (src.name + ".o")  # suffix kept: foo.hip and foo.cpp get distinct objects
     if force or not obj.exists() or obj.stat().st_mtime < max(src.stat().st_mtime, _headers()):
         cc = os.environ.get("CXX", "g++") if src.suffix == ".cpp" else HIPCC
         cmd = [cc, *_flags(src), "-c", str(src), "-o", str(obj)]

@@ -50,6 +50,13 @@ struct Prepared {
   bool sched_used = false;
   int ring_next = 0;
   int64_t delta_uploads = 0;
+  // The device delta holds grants of a plan that was never committed (its
+  // launch failed, or the caller did not commit).  Every launch applies the
+  // delta it finds, so the next plan uploads its own delta even without
+  // grants (all -1): otherwise a later launch would write a page into the
+  // table that the host pool still counts as free.  A committed delta may
+  // stay: re-applying it rewrites an entry the table already holds.
+  bool delta_uncommitted = false;
   bool pending = false;            // a planned step awaiting moba_prep_commit
   int64_t pending_version = 0;
   std::vector<int32_t> delta;      // [2 * rows] of the current plan
@@ -304,13 +311,15 @@ extern "C" int moba_prep_plan(void* h, int append, void* stream, int32_t* positi
       if (positions[i] < 0) return fail(MOBA_ERR_ARG, "query positions must refer to cached tokens");
     }
   }
-  if (grants) {
+  if (!append) std::fill(p->delta.begin(), p->delta.end(), -1);  // an attend grants nothing
+  if (grants || p->delta_uncommitted) {
     const int slot = p->ring_next;
     p->ring_next = (slot + 1) % kRing;
     rc = stage_copy(d.delta, p->pinned + (size_t)slot * 2 * d.rows, p->ring_ev[slot],
                     p->ring_used[slot], p->delta.data(), 2 * (size_t)d.rows, st);
     if (rc) return rc;
     ++p->delta_uploads;
+    p->delta_uncommitted = grants != 0;
   }
   if ((rc = refresh_schedule(*p, positions, st))) return rc;
   p->pending = append != 0;
@@ -336,8 +345,10 @@ extern "C" int moba_prep_commit(void* h) {
   if (!p) return fail(MOBA_ERR_ARG, "prep_commit: null handle");
   if (!p->pending) return MOBA_OK;
   p->pending = false;
-  return moba_pool_commit_step(p->d.lease, p->ids.data(), p->d.rows, p->delta.data(),
-                               p->pending_version);
+  const int rc = moba_pool_commit_step(p->d.lease, p->ids.data(), p->d.rows, p->delta.data(),
+                                       p->pending_version);
+  if (rc == MOBA_OK) p->delta_uncommitted = false;
+  return rc;
 }
 
 extern "C" int moba_prep_run(void* h, int append, int use_graph, void* stream,

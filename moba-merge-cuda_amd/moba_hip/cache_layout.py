@@ -181,7 +181,13 @@ class PageAllocator:
         ids = self._pool.ids(_slot_ids(sequence_ids), True)
         if len(ids) != len(counts):
             raise ValueError("one token count per sequence required")
-        cnt = np.asarray([positive_int(n, "append count") for n in counts], dtype=_I32)
+        counts = [positive_int(n, "append count") for n in counts]
+        # the length bound is checked before any buffer is sized by the counts
+        # (the native plan checks it again, together with the pool's capacity)
+        lengths = self._pool.length_view
+        if any(int(lengths[s]) + n > self.max_seq_len for s, n in zip(ids.tolist(), counts)):
+            raise ValueError("append exceeds max_seq_len")
+        cnt = np.asarray(counts, dtype=_I32)
         tokens = int(cnt.sum())
         seq = np.empty(tokens, _I32)
         pos = np.empty(tokens, _I32)

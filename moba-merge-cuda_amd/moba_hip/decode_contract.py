@@ -82,8 +82,12 @@ def finite(t, name):
 def tensors(specs, *, device, dtype, head_dim):
     """`tensor` for each (t, name, kwargs) in order, raising what those calls
     in sequence would raise first; the NaN/Inf test of all inputs reads one
-    flag (one host synchronisation instead of one per tensor)."""
+    flag (one host synchronisation instead of one per tensor).  A callable
+    `tokens` is evaluated only once the inputs before it passed their checks
+    (so `lambda: k.shape[0]` never reads an unchecked k)."""
     for i, (t, name, kw) in enumerate(specs):
+        if callable(kw.get("tokens")):
+            kw = dict(kw, tokens=kw["tokens"]())
         try:
             tensor(t, name, device=device, dtype=dtype, head_dim=head_dim, finite=False, **kw)
         except ValueError:

@@ -150,7 +150,7 @@ class PagedKVCache:
         with self._lock, torch.cuda.device(self.device):
             self._guard()
             self._check_inputs((k, "k", {"heads": self.num_kv_heads}),
-                               (v, "v", {"heads": self.num_kv_heads, "tokens": k.shape[0]}))
+                               (v, "v", {"heads": self.num_kv_heads, "tokens": lambda: k.shape[0]}))
             self._no_pool_alias(k, v)
             ids = self._layout.validate_ids(_ints(sequence_ids, "sequence_ids"), unique=True)
             counts = contract.append_counts(k.shape[0], ids, cu_seqlens)
@@ -240,8 +240,8 @@ class PagedKVCache:
             self._guard()
             dense = _mode(mode, topk)
             self._check_inputs((k, "k", {"heads": self.num_kv_heads}),
-                               (v, "v", {"heads": self.num_kv_heads, "tokens": k.shape[0]}),
-                               (q, "q", {"tokens": k.shape[0]}))
+                               (v, "v", {"heads": self.num_kv_heads, "tokens": lambda: k.shape[0]}),
+                               (q, "q", {"tokens": lambda: k.shape[0]}))
             self._no_pool_alias(q, k, v)
             contract.query_grid(q, self.num_kv_heads)
             ids = self._layout.validate_ids(_ints(sequence_ids, "sequence_ids"), unique=True)

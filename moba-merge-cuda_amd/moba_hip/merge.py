@@ -49,7 +49,11 @@ def merge_forward(self_out, self_lse, remote_out, remote_lse, mapping, kmax=None
     if kmax is None:
         kmax = 1
         if M:
-            kmax = max(1, int(torch.bincount(mapping.long(), minlength=P).max().item()))
+            # entries outside [0, P) are counted apart (bin P), so the
+            # kernel's range check reports them rather than bincount
+            m = mapping.long()
+            m = torch.where((m >= 0) & (m < P), m, torch.full_like(m, P))
+            kmax = max(1, int(torch.bincount(m, minlength=P + 1)[:P].max().item()))
     kmax = int(kmax)
     if not 1 <= kmax <= 8:
         raise RuntimeError("kmax must be in [1,8]")

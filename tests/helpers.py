@@ -53,10 +53,9 @@ def assert_grad_close(actual, expected, dtype, what="", max_tol=None):
     output dtype is within the max-abs bound (|ref| < 4 for bf16, < 8 for
     fp16).  An entry above that cannot be stored closer than half an ulp, so
     it is held to max-abs + one ulp of |ref| instead; such entries are counted
-    in the message.  The mean-abs bound applies to the small entries, to the
-    error in excess of the mean error of the FP64 reference itself stored in
-    the output dtype (entries of magnitude 1-4 already carry a mean storage
-    error of 1-4e-3 in bf16, beyond any kernel's control)."""
+    in the message.  The mean-abs bound applies, raw, to the small entries
+    (the mean of the FP64 reference's own storage error is logged beside it
+    for context)."""
     a = actual.detach().double().cpu().numpy() if isinstance(actual, torch.Tensor) else actual
     e = np.asarray(expected, dtype=np.float64)
     max_tol, mean_tol = (TOL[dtype][0] if max_tol is None else max_tol), TOL[dtype][1]
@@ -72,11 +71,9 @@ def assert_grad_close(actual, expected, dtype, what="", max_tol=None):
     if small.size:
         assert small.max() <= max_tol, \
             f"{what}: max abs {small.max():.3e} > {max_tol} ({n_big} entries above the ulp bound)"
-        stored = torch.from_numpy(e[~big]).to(dtype).double().numpy()
-        floor = float(np.abs(stored - e[~big]).mean())
-        assert small.mean() - floor <= mean_tol, \
-            (f"{what}: mean abs {small.mean():.3e} exceeds the storage rounding's {floor:.3e} "
-             f"by more than {mean_tol} ({n_big} entries above the ulp bound)")
+        assert small.mean() <= mean_tol, \
+            (f"{what}: mean abs {small.mean():.3e} > {mean_tol} "
+             f"({n_big} entries above the ulp bound)")
     if n_big:
         excess = diff[big] - (max_tol + ulp[big])
         assert excess.max() <= 0, \

@@ -50,6 +50,11 @@ def test_exhaustion_and_invalid_append_are_atomic():
         with pytest.raises(ValueError):
             a.plan_append(ids, counts)
         assert state(a) == before
+    # a huge count is refused by the length bound before anything is sized by it
+    for n in (2 ** 31 - 1, 2 ** 40):
+        with pytest.raises(ValueError, match="exceeds max_seq_len"):
+            a.plan_append([0], [n])
+        assert state(a) == before
 
 
 def test_closed_chunks_follow_logical_positions():

@@ -83,6 +83,27 @@ def test_decode_mode_contract(mode, topk):
         _mode(mode, topk)
 
 
+@pytest.mark.parametrize("bad", [None, torch.zeros(()), torch.zeros(4, 2)])
+def test_decode_input_checks_run_in_argument_order(bad):
+    """The NaN/Inf-batched checks of append / append_and_attend: a malformed
+    k raises the [N,H,D] ValueError (kv_cache.py:166-167 in the reference)
+    before the token counts of v and q, which depend on k, are looked at."""
+    from moba_hip import decode_contract as contract
+    v = torch.zeros(3, 2, 8)
+    kw = dict(device=torch.device("cpu"), dtype=torch.float32, head_dim=8)
+    for specs in (
+        ((bad, "k", {"heads": 2}), (v, "v", {"heads": 2, "tokens": lambda: bad.shape[0]})),
+        ((bad, "k", {"heads": 2}), (v, "v", {"heads": 2, "tokens": lambda: bad.shape[0]}),
+         (v, "q", {"tokens": lambda: bad.shape[0]})),
+    ):
+        with pytest.raises(ValueError, match=r"k must be \[N,H,D\]"):
+            contract.tensors(specs, **kw)
+    k = torch.zeros(2, 2, 8)
+    with pytest.raises(ValueError, match="v token count differs"):
+        contract.tensors(((k, "k", {"heads": 2}), (v, "v", {"heads": 2, "tokens": lambda: k.shape[0]})),
+                         **kw)
+
+
 def _declared_symbols():
     text = (ROOT / "include" / "moba_hip.h").read_text()
     return sorted(set(re.findall(r"\b(moba_(?:hip|pool|prep)_\w+)\s*\(", text)))

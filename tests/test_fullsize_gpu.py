@@ -177,13 +177,15 @@ def test_decode_full_size(cuda_device, batch, hq, hkv, d, page, chunk, topk, lo,
             check(cache, plan.step(q, kn, vn), q)
 
 
-@pytest.mark.parametrize("batch,hq,hkv,d,page,chunk,topk,lo,hi,dtype", [
-    (8, 12, 2, 128, 48, 512, 4, 2048, 16384, torch.bfloat16),   # cfg4
-    (32, 16, 1, 96, 64, 1024, 8, 1024, 32768, torch.float16),   # cfg5
+@pytest.mark.parametrize("batch,hq,hkv,d,page,chunk,topk,lo,hi,dtype,steps", [
+    (8, 12, 2, 128, 48, 512, 4, 2048, 16384, torch.bfloat16, 128),   # cfg4: 128 steps
+    (32, 16, 1, 96, 64, 1024, 8, 1024, 32768, torch.float16, 256),   # cfg5: 256 captured steps
 ])
-def test_decode_full_size_graph(cuda_device, batch, hq, hkv, d, page, chunk, topk, lo, hi, dtype):
-    """The captured step at the benchmark shapes: 24 graph replays on one
-    cache equal 24 eager steps on an identical cache bit for bit (outputs,
+def test_decode_full_size_graph(cuda_device, batch, hq, hkv, d, page, chunk, topk, lo, hi, dtype,
+                                steps):
+    """The captured step at the benchmark shapes, for the configs' own step
+    counts: every graph replay on one cache equals the eager step on an
+    identical cache bit for bit (outputs,
     LSE, routes, and afterwards the closed-chunk means and lengths), with
     eager work between the replays; rows 0 and 1 close a chunk during the run
     (a closing mean inside the replayed graph).  The last replay is also
@@ -192,7 +194,6 @@ def test_decode_full_size_graph(cuda_device, batch, hq, hkv, d, page, chunk, top
     lengths = [rng.randint(lo, hi) for _ in range(batch)]
     lengths[0] = (lengths[0] // chunk) * chunk + chunk - 5   # closes a chunk at step 5
     lengths[1] = (lengths[1] // chunk) * chunk + chunk - 17  # ... and at step 17
-    steps = 24
     caches = [_decode_cache(batch, lengths, hkv, d, page, chunk, dtype, steps + 8, seed=31)
               for _ in range(2)]
     g = torch.Generator(device="cuda").manual_seed(32)

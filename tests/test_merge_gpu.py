@@ -99,5 +99,9 @@ def test_merge_capacity_and_range_errors(cuda_device):
     merge_forward(so, sl, ro, rl, crowded, kmax=2, check_capacity=False)  # no raise
     with pytest.raises(RuntimeError, match=r"\[0,T\*H\)"):
         merge_forward(so, sl, ro, rl, torch.tensor([0, 1, 8, 2, 3], device="cuda"))
+    # negative and far-out entries with the derived kmax reach the same native check
+    for bad in ([0, -1, 2, 3, 4], [0, 1, 2, 3, 1 << 40], [-5, -5, -5, -5, -5]):
+        with pytest.raises(RuntimeError, match=r"\[0,T\*H\)"):
+            merge_forward(so, sl, ro, rl, torch.tensor(bad, device="cuda"))
     with pytest.raises(ValueError, match="deterministic"):
         merge_forward(so, sl, ro, rl, crowded, deterministic=1)

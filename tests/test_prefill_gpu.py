@@ -343,3 +343,42 @@ def test_side_stream_orders_after_its_producers(cuda_device):
     torch.cuda.synchronize()
     for a, b in zip(got, ref):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("hq,hkv,lens,chunk,topk", [
+    (8, 2, (300, 200), 32, 4),        # two sequences: filtered index = chunk - its batch
+    (4, 4, (96, 1, 161, 64), 16, 3),  # a 1-token sequence and an exact multiple of the chunk
+])
+def test_route_hook_matches_oracle(cuda_device, hq, hkv, lens, chunk, topk):
+    """ROUTE_HOOK (grouped_attention.py:72-74 in the reference, used by
+    tests/test_attention_opt.py:68-74) receives cu_chunk, the filtered chunk
+    indices, chunk_to_batch and selected [F,Hq,T] bool equal to the oracle's
+    calc_chunks and to the mask of the oracle's routes, on multi-sequence
+    batches; it is called once per forward and never when unset."""
+    import moba_hip
+    from moba_hip import grouped_attention as GA
+    q, k, v, cu, ml, _ = prefill_inputs(hq, hkv, 64, lens, torch.bfloat16, seed=29)
+    cfg = {"chunk_size": chunk, "topk": topk}
+    calls = []
+    GA.ROUTE_HOOK = lambda **kw: calls.append({n: t.cpu() for n, t in kw.items()})
+    try:
+        moba_hip.run_impl("opt_hip", q, k, v, cu, ml, cfg)
+    finally:
+        GA.ROUTE_HOOK = None
+    assert len(calls) == 1
+    got = calls[0]
+    assert set(got) == {"cu_chunk", "filtered_chunk_indices", "chunk_to_batch", "selected"}
+    sel, _, _, (cu_chunk, chunk_batch, filtered, _) = oracle_route(q, k, cu, chunk, topk)
+    assert got["cu_chunk"].tolist() == list(cu_chunk)
+    assert got["filtered_chunk_indices"].tolist() == list(filtered)
+    assert got["chunk_to_batch"].tolist() == list(chunk_batch)
+    T = q.shape[0]
+    want = np.zeros((len(filtered), hq, T), dtype=bool)
+    f_of = {c: f for f, c in enumerate(filtered)}
+    for s, h, j in zip(*np.nonzero(sel >= 0)):
+        want[f_of[int(sel[s, h, j])], h, s] = True
+    assert got["selected"].dtype == torch.bool
+    np.testing.assert_array_equal(got["selected"].numpy(), want)
+    assert want.any() and not want.all()
+    moba_hip.run_impl("opt_hip", q, k, v, cu, ml, cfg)   # unset: not called again
+    assert len(calls) == 1

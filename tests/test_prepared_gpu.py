@@ -277,3 +277,30 @@ def test_step_input_errors_follow_argument_order(cuda_device):
         assert cache.lengths == lengths
         r = p.step(q, kn, vn)
         assert cache.lengths == tuple(n + 1 for n in lengths) and r.output.isfinite().all()
+
+
+@pytest.mark.parametrize("graph", [False, True])
+def test_uncommitted_page_grant_never_reaches_the_table(cuda_device, graph):
+    """A step planned at a page boundary whose launch never ran (as after a
+    failed launch: the plan uploaded its page grant, nothing committed it)
+    must not leave that grant on the device: the next attend and step apply
+    a clean delta, so the device page table keeps matching the host pool."""
+    from moba_hip.ops import _lib  # noqa: F401
+    c = _paged()(1, 12, 1, 8, page_size=3, chunk_size=4)
+    k = rand((3, 1, 8), c.dtype, 901)
+    c.append(k, k, sequence_ids=[0], cu_seqlens=[0, 3])
+    q = rand((1, 2, 8), c.dtype, 902)
+    with c.prepare_decode([0], 2) as p:
+        if graph:
+            p.capture("attend").capture("step")
+        stream = torch.cuda.current_stream().cuda_stream
+        assert p._plan_step(stream) == (3,)   # token 3 opens logical page 1: a grant
+        p.attend(q, use_graph=graph)          # no launch or commit of the step above
+        torch.cuda.synchronize()
+        host = [list(r) for r in p.page_table]
+        assert host[0][1] == -1
+        assert c._table[0].tolist()[:len(host[0])] == host[0]
+        kn = rand((1, 1, 8), c.dtype, 903)
+        check(c, p.step(q, kn, kn, use_graph=graph), q)
+        torch.cuda.synchronize()
+        assert c._table[0].tolist()[:len(host[0])] == [list(r) for r in p.page_table][0]
