@@ -248,9 +248,18 @@ int moba_hip_decode_step(int* table, int table_width, int* lengths, const int* i
                          int dtype, void* k_cache, void* v_cache, int page_size, int Hkv, int D,
                          int chunk, void* means, int max_chunks, void* stream);
 
-/* 1 when moba_hip_decode_fused handles this shape: Hq/Hkv <= 16, D a
- * multiple of 8 in [8,256], a page table of at most 2048 entries per row and
- * a route width whose scratch fits LDS. */
+/* Virtual kv heads per kv head of moba_hip_decode_fused: the fewest Vg that
+ * cut the Hq/Hkv q heads of a kv head into equal groups of at most 16 (1 up
+ * to 16 q heads per kv head, 2 up to 32, ...); 0 when Hq is not a multiple
+ * of Hkv.  The reference's kernel takes any group size in one program per
+ * (query, q head) (paged_decode.py:67-112); here a group of at most 16 q
+ * heads shares one pass over the K/V the group selected. */
+int moba_hip_decode_fused_groups(int Hq, int Hkv);
+
+/* 1 when moba_hip_decode_fused handles this shape: Hq a multiple of Hkv, D a
+ * multiple of 8 in [8,256], and a route width and page-table width
+ * (table_width entries per row, staged in LDS) whose scratch fits the
+ * launch's 64 KiB of dynamic LDS. */
 int moba_hip_decode_fused_supported(int Hq, int Hkv, int D, int width, int table_width);
 
 /* Whole decode for Nq query rows (one query per row), two launches on the
@@ -271,10 +280,13 @@ int moba_hip_decode_fused_supported(int Hq, int Hkv, int D, int width, int table
  *             new token k/v [Nq,Hkv,D] is scattered into the pool, the mean of
  *             the chunk it closes is written to means (canonical order, as
  *             moba_hip_block_means), and lengths advance by one.
- * splits S in [1,64] workgroups per (row, kv head), or, with a schedule
- * sched (may be null), at most S: sched holds n_sched workgroup entries
- * (row * Hkv + kv head, split, splits of that row), every split of every
- * (row, kv head) exactly once, followed by the Nq*Hkv split counts.
+ * The workgroups of a row are laid out per virtual kv head: Hv = Hkv * Vg
+ * (Vg = moba_hip_decode_fused_groups(Hq, Hkv)), virtual head u serving q
+ * heads u*G .. u*G+G-1 (G = Hq/Hv) against physical kv head u / Vg.
+ * splits S in [1,64] workgroups per (row, virtual kv head), or, with a
+ * schedule sched (may be null), at most S: sched holds n_sched workgroup
+ * entries (row * Hv + virtual head, split, splits of that row), every split of
+ * every (row, virtual head) exactly once, followed by the Nq*Hv split counts.
  * Workspaces part_o [Nq*Hq*S, D] and part_ml [Nq*Hq*S, 2] fp32.  width must
  * be >= max(position) / chunk.  Outputs are deterministic for a fixed
  * schedule.
@@ -292,7 +304,7 @@ int moba_hip_decode_fused(const void* q, const void* k, const void* v, int dtype
  * capture, tight serving loops, harnesses that forbid hipMalloc).  No
  * counterpart in the reference.  Same as moba_hip_decode_fused with
  * pos_mode 0 (positions given; nothing in the cache changes) and the uniform
- * split count S = clamp(ceil(256 / (Nq*Hkv)), 1, 64), but the split partials
+ * split count S = clamp(ceil(256 / (Nq*Hv)), 1, 64), but the split partials
  * live in a static per-device scratch array of 8 MiB instead of caller
  * workspaces: calls needing more than Nq*Hq*S*(D+2)*4 (+256) bytes fail
  * with MOBA_ERR_CAPACITY before launching anything.  It calls no allocating

@@ -71,7 +71,8 @@ constexpr int kFwNarrow = 8;
 constexpr int kFwWide = 12;
 constexpr int kWideBlocksPerWorkgroup = 16;  // expected blocks at which 12 waves pay
 constexpr int kMaxSlots = 9;    // current chunk + up to 8 routed chunks
-constexpr int kTblMax = 2048;   // page-table entries staged in LDS
+constexpr int kGroupMax = 16;   // q heads of one (virtual) kv-head group: the MFMA's 16 columns
+constexpr size_t kDynMax = 64 * 1024;  // dynamic LDS of one launch (route scratch + table row)
 
 struct FusedArgs {
   const uint16_t* q;   // [Nq, Hq, D]
@@ -79,7 +80,11 @@ struct FusedArgs {
   const uint16_t* v;
   uint16_t* kc;        // pool [pages, P, Hkv, D]
   uint16_t* vc;
-  int Nq, Hq, Hkv, D, G, P, W, C, width, R, max_chunks, dense, pos_mode;
+  // G: q heads per workgroup group (<= 16).  A kv head with more q heads is
+  // served as Vg virtual kv heads of G q heads each (Vg * G = Hq / Hkv):
+  // they share the physical head's K/V, means and page table, and the first
+  // of them does the kv head's side work (scatter, closing mean).
+  int Nq, Hq, Hkv, Vg, D, G, P, W, C, width, R, max_chunks, dense, pos_mode;
   float scale_log2;
   int* table;          // [B, W]
   int* lengths;        // [B]
@@ -99,10 +104,10 @@ struct FusedArgs {
 
 // Route scratch in dynamic LDS (ints / floats):
 //   sc[G * width] | umask[width + 1] | item_c[width + 1] | item_m[width + 1] |
-//   bp[width + 2] | sel[16 * kMaxSlots] | table row [kTblMax]
-inline size_t fused_route_lds(int G, int width) {
-  return sizeof(int) *
-         ((size_t)G * width + 3 * (size_t)(width + 1) + (width + 2) + 16 * kMaxSlots + kTblMax);
+//   bp[width + 2] | sel[16 * kMaxSlots] | table row [table width, rounded up to 4]
+inline size_t fused_route_lds(int G, int width, int table_width) {
+  return sizeof(int) * ((size_t)G * width + 3 * (size_t)(width + 1) + (width + 2) +
+                        16 * kMaxSlots + (((size_t)table_width + 3) & ~(size_t)3));
 }
 
 // Static LDS of fused_kernel<., DP, FW>: the per-wave V tiles (rows of
@@ -143,8 +148,11 @@ __global__ __launch_bounds__(64 * FW) void fused_kernel(FusedArgs a) {
   } else {
     split = blockIdx.x; S = gridDim.x; rowk = blockIdx.y;
   }
-  const int qrow = rowk / a.Hkv, kh = rowk % a.Hkv;
+  const int Hv = a.Hkv * a.Vg;  // (virtual) kv heads per row
+  const int qrow = rowk / Hv, vh = rowk % Hv, kh = vh / a.Vg;
   const int G = a.G, D = a.D, C = a.C, width = a.width;
+  const int hb = vh * G;                // first q head of the group
+  const bool lead = vh % a.Vg == 0;     // does the physical kv head's side work
 
   DTRACE(0);
   // Row state comes from uniform (scalar) loads; the loads that need only the
@@ -183,7 +191,7 @@ __global__ __launch_bounds__(64 * FW) void fused_kernel(FusedArgs a) {
 #pragma unroll
     for (int i = 0; i < NQ; ++i) {
       const int x = tid + i * 64 * kFW, qg = x / RC, qj = x % RC;
-      qv[i] = ld8(a.q + ((int64_t)qrow * a.Hq + kh * G + min(qg, G - 1)) * D +
+      qv[i] = ld8(a.q + ((int64_t)qrow * a.Hq + hb + min(qg, G - 1)) * D +
                   min(qj, D / 8 - 1) * 8);
       if (!(qg < G && qj * 8 < D)) qv[i] = zero8();
     }
@@ -207,7 +215,7 @@ __global__ __launch_bounds__(64 * FW) void fused_kernel(FusedArgs a) {
   const bool step = a.pos_mode == 2;
   // the position is published for the merge launch before any early exit (no
   // workgroup of this launch reads it in prepared modes)
-  if (a.pos_mode != 0 && split == 0 && kh == 0 && tid == 0) a.positions[qrow] = p;
+  if (a.pos_mode != 0 && split == 0 && vh == 0 && tid == 0) a.positions[qrow] = p;
   if (p < 0 || p / C > width) return;  // caller contract: width covers every position
   const int npg = min(p / a.P + 1, a.W);
   const int cur = p / C;  // the current chunk (always attended, by every head)
@@ -241,9 +249,9 @@ __global__ __launch_bounds__(64 * FW) void fused_kernel(FusedArgs a) {
   auto page_at = [&](int slot) -> int { return slot == dl ? dp : tbl[slot]; };
 
   // ---- side work of a step: table delta + scatter (split 0), closing mean
-  if (a.pos_mode != 0 && split == 0 && kh == 0 && tid == 0 && dl >= 0)
+  if (a.pos_mode != 0 && split == 0 && vh == 0 && tid == 0 && dl >= 0)
     a.table[(int64_t)sid * a.W + dl] = dp;
-  if (step && split == 0) {
+  if (step && split == 0 && lead) {
     const int page = page_at(p / a.P);
     if (page >= 0) {
       const int64_t dst = (((int64_t)page * a.P + p % a.P) * a.Hkv + kh) * D;
@@ -254,7 +262,7 @@ __global__ __launch_bounds__(64 * FW) void fused_kernel(FusedArgs a) {
       }
     }
   }
-  if (step && (p + 1) % C == 0) {
+  if (step && lead && (p + 1) % C == 0) {
     // The mean of the chunk this token closes, canonical order: lane j sums
     // tokens j, j+64, ... of the chunk in order, then the fixed tree.  Its
     // D/8 items of 8 dims are spread over the row's splits and waves (item i:
@@ -393,7 +401,7 @@ __global__ __launch_bounds__(64 * FW) void fused_kernel(FusedArgs a) {
   if (!a.dense && split == 0 && a.selected != nullptr) {
     for (int x = tid; x < G * S1; x += 64 * kFW) {
       const int g = x / S1, j = x % S1;
-      a.selected[((int64_t)qrow * a.Hq + kh * G + g) * S1 + j] = sel_s[x];
+      a.selected[((int64_t)qrow * a.Hq + hb + g) * S1 + j] = sel_s[x];
     }
   }
   // items: the union's chunks in ascending order with their head masks, and
@@ -436,7 +444,7 @@ __global__ __launch_bounds__(64 * FW) void fused_kernel(FusedArgs a) {
   // ---- attention over blocks [b0, b1)
   uint16_t* Vs = reinterpret_cast<uint16_t*>(lds) + w * STAGE;
   const bool head_ok = c16 < G;
-  const int h = kh * G + (head_ok ? c16 : 0);
+  const int h = hb + (head_ok ? c16 : 0);
   u16x8_t qf[NKS];
   {
     const uint16_t* qp = a.q + ((int64_t)qrow * a.Hq + h) * D;
@@ -654,7 +662,7 @@ __global__ __launch_bounds__(64 * FW) void fused_kernel(FusedArgs a) {
     const float iz = z > 0.0f ? 1.0f / z : 0.0f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) acc[e] *= iz;
-    const int64_t entry = ((int64_t)qrow * a.Hq + kh * G + g) * a.smax + split;
+    const int64_t entry = ((int64_t)qrow * a.Hq + hb + g) * a.smax + split;
     *reinterpret_cast<f32x4_t*>(a.part_o + entry * D + d) = acc;
     if (d == 0) { a.part_ml[2 * entry] = M; a.part_ml[2 * entry + 1] = z; }
   }
@@ -677,7 +685,7 @@ template <int DT>
 __global__ __launch_bounds__(64 * kMergeWaves) void merge_kernel(FusedArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int rh = blockIdx.x, qrow = rh / a.Hq, h = rh % a.Hq;
-  const int S = a.sched != nullptr ? a.sched[3 * a.n_sched + qrow * a.Hkv + h / a.G] : a.smax;
+  const int S = a.sched != nullptr ? a.sched[3 * a.n_sched + qrow * a.Hkv * a.Vg + h / a.G] : a.smax;
   // the row's position decides only whether anything is written: its loads
   // (ids -> lengths) run beside the partial loads below, which stay inside
   // the row's own slots either way
@@ -762,14 +770,14 @@ bool wide_launch(const FusedArgs& a, int splits, int DP, size_t dyn) {
   if (dyn + fused_static_lds(DP, kFwWide) > kLdsBytes) return false;
   const int64_t chunks = a.dense ? a.width : std::min(a.width, a.R + 1);
   const int64_t blocks = chunks * ((a.C + 31) / 32);
-  const int64_t per_row = a.sched != nullptr ? std::max(1, a.n_sched / (a.Nq * a.Hkv)) : splits;
+  const int64_t per_row = a.sched != nullptr ? std::max(1, a.n_sched / (a.Nq * a.Hkv * a.Vg)) : splits;
   return blocks >= (int64_t)kWideBlocksPerWorkgroup * per_row;
 }
 
 template <int DT, int DP>
 int launch_fused(const FusedArgs& a, int splits, size_t dyn, hipStream_t st) {
   const dim3 grid = a.sched != nullptr ? dim3((unsigned)a.n_sched)
-                                        : dim3((unsigned)splits, (unsigned)(a.Nq * a.Hkv));
+                                        : dim3((unsigned)splits, (unsigned)(a.Nq * a.Hkv * a.Vg));
   bool wide = false;
   if constexpr (DP <= 128) {
     wide = wide_launch(a, splits, DP, dyn);
@@ -805,12 +813,20 @@ int uniform_splits(int Nq, int Hkv) {
 }
 }  // namespace
 
+extern "C" int moba_hip_decode_fused_groups(int Hq, int Hkv) {
+  if (Hkv < 1 || Hq < 1 || Hq % Hkv) return 0;
+  const int G = Hq / Hkv;
+  for (int vg = (G + kGroupMax - 1) / kGroupMax; vg <= G; ++vg)
+    if (G % vg == 0) return vg;  // the fewest groups of equal size <= 16
+  return 0;
+}
+
 extern "C" int moba_hip_decode_fused_supported(int Hq, int Hkv, int D, int width, int table_width) {
-  if (Hkv < 1 || Hq % Hkv || Hq / Hkv > 16 || D % 8 || D < 8 || D > 256) return 0;
-  if (table_width < 1 || table_width > kTblMax) return 0;
+  const int vg = moba_hip_decode_fused_groups(Hq, Hkv);
+  if (vg < 1 || D % 8 || D < 8 || D > 256 || table_width < 1 || width < 0) return 0;
   const int DP = D <= 32 ? 32 : D <= 64 ? 64 : D <= 96 ? 96 : D <= 128 ? 128 : 256;
-  const size_t dyn = fused_route_lds(Hq / Hkv, width);
-  return dyn <= 64 * 1024 && dyn + fused_static_lds(DP, kFwNarrow) <= kLdsBytes ? 1 : 0;
+  const size_t dyn = fused_route_lds(Hq / Hkv / vg, width, table_width);
+  return dyn <= kDynMax && dyn + fused_static_lds(DP, kFwNarrow) <= kLdsBytes ? 1 : 0;
 }
 
 extern "C" int moba_hip_decode_fused(const void* q, const void* k, const void* v, int dtype, int Nq,
@@ -824,19 +840,22 @@ extern "C" int moba_hip_decode_fused(const void* q, const void* k, const void* v
                                      void* stream) {
   if (dtype != 0 && dtype != 1) { moba_set_error("decode_fused: dtype must be 0 (bf16) or 1 (fp16)"); return MOBA_ERR_ARG; }
   if (!moba_hip_decode_fused_supported(Hq, Hkv, D, width, table_width)) {
-    moba_set_error("decode_fused: needs Hq/Hkv <= 16, head_dim a multiple of 8 in [8,256], a table width <= 2048 and a route width that fits LDS");
+    moba_set_error("decode_fused: needs Hq a multiple of Hkv, head_dim a multiple of 8 in [8,256], "
+                   "and a route width and page-table width that fit LDS");
     return MOBA_ERR_CAPACITY;
   }
   if (R < 0 || R + 1 > kMaxSlots) { moba_set_error("decode_fused: routed chunk count must be in [0,8]"); return MOBA_ERR_ARG; }
   if (pos_mode < 0 || pos_mode > 2) { moba_set_error("decode_fused: pos_mode must be 0 (given), 1 (attend) or 2 (step)"); return MOBA_ERR_ARG; }
   if (splits < 1 || splits > 64) { moba_set_error("decode_fused: splits must be in [1,64]"); return MOBA_ERR_ARG; }
-  if (sched != nullptr && n_sched < Nq * Hkv) { moba_set_error("decode_fused: a schedule needs at least one workgroup per (row, kv head)"); return MOBA_ERR_ARG; }
+  const int vg = moba_hip_decode_fused_groups(Hq, Hkv);
+  if (sched != nullptr && n_sched < Nq * Hkv * vg) { moba_set_error("decode_fused: a schedule needs at least one workgroup per (row, kv head)"); return MOBA_ERR_ARG; }
   if (page_size < 1 || chunk < 1 || width < 0 || Nq < 1) { moba_set_error("decode_fused: bad sizes"); return MOBA_ERR_ARG; }
   if (pos_mode == 2 && (k == nullptr || v == nullptr)) { moba_set_error("decode_fused: step mode needs the new K/V rows"); return MOBA_ERR_ARG; }
   FusedArgs a;
   a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v;
   a.kc = (uint16_t*)k_cache; a.vc = (uint16_t*)v_cache;
-  a.Nq = Nq; a.Hq = Hq; a.Hkv = Hkv; a.D = D; a.G = Hq / Hkv; a.P = page_size; a.W = table_width;
+  a.Nq = Nq; a.Hq = Hq; a.Hkv = Hkv; a.Vg = vg; a.D = D; a.G = Hq / Hkv / vg; a.P = page_size;
+  a.W = table_width;
   a.C = chunk; a.width = width; a.R = dense ? 0 : R; a.max_chunks = max_chunks; a.dense = dense;
   a.pos_mode = pos_mode;
   a.scale_log2 = kLog2e / sqrtf((float)D);
@@ -844,7 +863,7 @@ extern "C" int moba_hip_decode_fused(const void* q, const void* k, const void* v
   a.means = (uint16_t*)means; a.selected = selected; a.part_o = part_o; a.part_ml = part_ml;
   a.out = (uint16_t*)out; a.lse = lse;
   a.sched = sched; a.n_sched = n_sched; a.smax = splits;
-  const size_t dyn = fused_route_lds(a.G, width);
+  const size_t dyn = fused_route_lds(a.G, width, table_width);
   hipStream_t st = (hipStream_t)stream;
   return dtype == 0 ? dispatch_fused<0>(a, splits, dyn, st) : dispatch_fused<1>(a, splits, dyn, st);
 }
@@ -895,7 +914,7 @@ extern "C" int moba_hip_decode_attend_noalloc(const void* q, int dtype, int Nq, 
                                               int dense, int* selected, void* out, float* lse,
                                               void* stream) {
   if (Nq < 1 || Hkv < 1 || Hq < 1 || D < 1) { moba_set_error("decode_attend_noalloc: bad sizes"); return MOBA_ERR_ARG; }
-  const int splits = uniform_splits(Nq, Hkv);
+  const int splits = uniform_splits(Nq, Hkv * std::max(1, moba_hip_decode_fused_groups(Hq, Hkv)));
   const int64_t rows = (int64_t)Nq * Hq * splits;
   const int64_t part_o_bytes = (rows * D * 4 + 255) / 256 * 256;
   const int64_t need = part_o_bytes + rows * 2 * 4;

@@ -225,10 +225,12 @@ int refresh_schedule(Prepared& p, const int32_t* pos, hipStream_t st) {
       near = (int64_t)std::abs(pos[i] - p.sched_pos[i]) * 8 <= std::max(p.sched_pos[i], 1);
     if (near) return MOBA_OK;
   }
-  const int n = 3 * d.n_sched + d.rows * d.hkv;
-  std::vector<int32_t> splits(d.rows * d.hkv);
+  // the fused launch's workgroups serve virtual kv heads of at most 16 q heads
+  const int hv = d.hkv * moba_hip_decode_fused_groups(d.hq, d.hkv);
+  const int n = 3 * d.n_sched + d.rows * hv;
+  std::vector<int32_t> splits(d.rows * hv);
   p.sched_entries.resize(n);
-  int rc = moba_prep_schedule(pos, d.rows, d.hkv, d.hq / d.hkv, d.remote, d.chunk, d.dense,
+  int rc = moba_prep_schedule(pos, d.rows, hv, d.hq / hv, d.remote, d.chunk, d.dense,
                               d.n_sched, d.splits, p.sched_entries.data(), splits.data());
   if (rc) return rc;
   if (splits != p.sched_splits) {
@@ -257,7 +259,8 @@ extern "C" int moba_prep_create(const MobaPrepDesc* desc, const int32_t* ids, vo
   const MobaPrepDesc& d = *desc;
   if (d.rows < 1 || d.hq < 1 || d.hkv < 1 || d.lease == nullptr)
     return fail(MOBA_ERR_ARG, "prep_create: bad descriptor");
-  if (d.fused && (d.splits < 1 || d.splits > 64 || (d.sched && d.n_sched < d.rows * d.hkv)))
+  const int hv = d.hkv * moba_hip_decode_fused_groups(d.hq, d.hkv);  // 0: not a fused shape
+  if (d.fused && (hv < 1 || d.splits < 1 || d.splits > 64 || (d.sched && d.n_sched < d.rows * hv)))
     return fail(MOBA_ERR_ARG, "prep_create: bad fused schedule sizes");
   Prepared* p = new (std::nothrow) Prepared;
   if (!p) return fail(MOBA_ERR_ARG, "prep_create: out of host memory");
@@ -267,7 +270,7 @@ extern "C" int moba_prep_create(const MobaPrepDesc* desc, const int32_t* ids, vo
   for (int i = 0; i < d.rows; ++i) p->ids_identity = p->ids_identity && ids[i] == i;
   p->delta.assign(2 * d.rows, -1);
   const size_t ring = (size_t)kRing * 2 * d.rows;
-  const size_t sched = d.fused && d.sched ? (size_t)3 * d.n_sched + d.rows * d.hkv : 0;
+  const size_t sched = d.fused && d.sched ? (size_t)3 * d.n_sched + (size_t)d.rows * hv : 0;
   hipError_t e = hipHostMalloc((void**)&p->pinned, (ring + sched + 1) * sizeof(int32_t),
                                hipHostMallocDefault);
   if (e != hipSuccess) { p->pinned = nullptr; release(p); return hip_fail("prep_create: pinned staging", e); }

@@ -46,6 +46,7 @@ SIGNATURES = {
     "moba_hip_decode_step": [_P, _I, _P, _P, _P, _P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P,
                              _I, _P],
     "moba_hip_decode_fused_supported": [_I, _I, _I, _I, _I],
+    "moba_hip_decode_fused_groups": [_I, _I],
     "moba_hip_decode_fused": [_P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _I, _P, _P, _P, _P,
                               _P, _I, _I, _I, _I, _I, _I, _I, _P, _I, _P, _P, _P, _P, _P, _P],
     "moba_hip_decode_attend_noalloc": [_P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _I, _P, _P, _P,

@@ -72,6 +72,12 @@ def fused_supported(hq, hkv, d, width, table_width) -> bool:
     return bool(_lib.load().moba_hip_decode_fused_supported(hq, hkv, d, width, table_width))
 
 
+def fused_heads(hq, hkv) -> int:
+    """(Virtual) kv heads per row of a fused launch: each kv head with more
+    than 16 q heads is served as equal groups of at most 16."""
+    return hkv * _lib.load().moba_hip_decode_fused_groups(hq, hkv)
+
+
 def fused_splits(nq, hkv) -> int:
     """Workgroups per (row, kv head): about one (8-wave workgroup) per CU
     over the whole launch."""
@@ -134,14 +140,15 @@ class FusedWork:
     __slots__ = ("splits", "part_o", "part_ml", "sched", "n_sched")
 
     def __init__(self, nq, hq, hkv, d, device, splits=None, scheduled=False):
-        self.splits = splits or (SCHED_MAX_SPLITS if scheduled else fused_splits(nq, hkv))
+        hv = fused_heads(hq, hkv)
+        self.splits = splits or (SCHED_MAX_SPLITS if scheduled else fused_splits(nq, hv))
         n = nq * hq * self.splits
         self.part_o = torch.empty((n, d), dtype=torch.float32, device=device)
         self.part_ml = torch.empty((n, 2), dtype=torch.float32, device=device)
         self.sched, self.n_sched = None, 0
         if scheduled:
-            self.n_sched = sched_workgroups(nq, hkv, max_splits=self.splits)
-            self.sched = torch.zeros(3 * self.n_sched + nq * hkv, dtype=torch.int32,
+            self.n_sched = sched_workgroups(nq, hv, max_splits=self.splits)
+            self.sched = torch.zeros(3 * self.n_sched + nq * hv, dtype=torch.int32,
                                      device=device)
 
 

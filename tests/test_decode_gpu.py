@@ -312,13 +312,16 @@ def test_unmapped_page_is_never_written(cuda_device):
     assert int(cache.k_cache.count_nonzero()) == 0 and int(cache.v_cache.count_nonzero()) == 0
 
 
-@pytest.mark.parametrize("dim", [136, 200, 256])
+@pytest.mark.parametrize("dim", [132, 200, 256])
 def test_wide_groups_wide_heads(cuda_device, dim):
-    """More than 16 q heads per kv head take the multi-kernel path; above 128
-    dims its attention workgroups run 4 waves.  Attend and append-and-attend
-    against the oracle, moba and dense."""
+    """32 q heads per kv head.  Head dims that are multiples of 8 take the
+    fused launch as two virtual kv heads of 16 q heads; 132 takes the
+    multi-kernel path, whose attention workgroups run 4 waves above 128 dims.
+    Attend and append-and-attend against the oracle, moba and dense."""
+    from moba_hip.ops import decode as kernels
     Paged, _ = _caches()
     cache = Paged(3, 200, 1, dim, page_size=9, chunk_size=16, dtype=torch.bfloat16)
+    assert kernels.fused_supported(32, 1, dim, 12, cache._table.shape[1]) == (dim % 8 == 0)
     k, v = rand((150, 1, dim), torch.bfloat16, 171), rand((150, 1, dim), torch.bfloat16, 172)
     cache.append(k, v, sequence_ids=[0, 1, 2], cu_seqlens=[0, 61, 100, 150])
     q = rand((3, 32, dim), torch.bfloat16, 173)
@@ -352,3 +355,37 @@ def test_input_errors_follow_argument_order(cuda_device):
     with pytest.raises(ValueError, match="k contains NaN/Inf"):
         cache.append(kn * nan, vn[:, :1], sequence_ids=[0])
     assert cache.lengths == lengths
+
+
+@pytest.mark.parametrize("graph", [False, True])
+@pytest.mark.parametrize("hq,hk,dim,dtype", [
+    (32, 1, 128, torch.bfloat16),   # 2 virtual kv heads of 16
+    (40, 2, 64, torch.float16),     # 2 of 10 per kv head
+    (24, 1, 96, torch.bfloat16),    # 2 of 12
+    (17, 1, 64, torch.bfloat16),    # 17 of 1 (a prime group)
+])
+def test_virtual_kv_heads_prepared(cuda_device, graph, hq, hk, dim, dtype):
+    """More than 16 q heads per kv head on the fused launch: prepared steps
+    (scatter, closing means and the length advance done once per physical
+    kv head) and attends, eager and replayed, against the oracle; rows close
+    chunks during the run."""
+    from moba_hip.ops import decode as kernels
+    Paged, _ = _caches()
+    vg = {32: 2, 20: 2, 24: 2, 17: 17}[hq // hk]
+    assert kernels.fused_heads(hq, hk) == hk * vg
+    cache = Paged(3, 120, hk, dim, page_size=5, chunk_size=8, dtype=dtype)
+    k, v = rand((90, hk, dim), dtype, 191), rand((90, hk, dim), dtype, 192)
+    cache.append(k, v, sequence_ids=[0, 1, 2], cu_seqlens=[0, 29, 61, 90])
+    assert kernels.fused_supported(hq, hk, dim, 14, cache._table.shape[1])
+    with cache.prepare_decode([2, 0, 1], hq, topk=4) as p:
+        assert p.fused
+        if graph:
+            p.capture("step").capture("attend")
+        for step in range(6):
+            q = rand((3, hq, dim), dtype, 200 + step)
+            kn, vn = rand((3, hk, dim), dtype, 210 + step), rand((3, hk, dim), dtype, 220 + step)
+            check(cache, p.step(q, kn, vn, use_graph=graph), q)
+            check(cache, p.attend(q, use_graph=graph), q)
+    assert cache.lengths == (35, 38, 35)
+    q = rand((3, hq, dim), dtype, 230)
+    check(cache, cache.attend(q, sequence_ids=[0, 1, 2], topk=4), q)

@@ -218,3 +218,42 @@ def test_decode_full_size_graph(cuda_device, batch, hq, hkv, d, page, chunk, top
     for row, n in enumerate(ends):  # the closed chunks' means (the rest is unwritten)
         closed = n // chunk
         assert torch.equal(caches[0]._means[row, :closed], caches[1]._means[row, :closed]), row
+
+
+@pytest.mark.parametrize("name,hq,hkv,dtype", [
+    ("P18", 32, 8, torch.bfloat16),
+    ("M06", 32, 1, torch.bfloat16),
+])
+def test_reference_decode_matrix_full_size(cuda_device, name, hq, hkv, dtype):
+    """Rows of the reference's decode matrix (configs/decode_perf.json: batch
+    16, 32K tokens, D 128, page 16, chunk 128, top-4) at full size on the
+    fused launch: the benchmark's step cache (max_seq_len = length + extra,
+    benchmarks/benchmark_decode.py:105-112) has a page table of 2049 entries
+    per row, and M06 has 32 q heads per kv head.  An attend, two prepared
+    steps and a replayed attend are checked against the oracle (means and
+    routes bit-equal, outputs vs FP64); the replay equals the eager attend
+    bit for bit."""
+    from moba_hip.ops import decode as kernels
+    batch, length, d, page, chunk, topk = 16, 32768, 128, 16, 128, 4
+    cache = _decode_cache(batch, [length] * batch, hkv, d, page, chunk, dtype, 8, seed=41)
+    assert cache._table.shape[1] == 2049
+    assert kernels.fused_supported(hq, hkv, d, length // chunk, cache._table.shape[1])
+    g = torch.Generator(device="cuda").manual_seed(42)
+    ids = list(range(batch))
+    q = torch.randn((batch, hq, d), generator=g, device="cuda").to(dtype)
+    check(cache, cache.attend(q, sequence_ids=ids, topk=topk), q)
+    with cache.prepare_decode(ids, hq, topk=topk) as p:
+        assert p.fused
+        p.capture("attend")
+        for _ in range(2):
+            q = torch.randn((batch, hq, d), generator=g, device="cuda").to(dtype)
+            kn = torch.randn((batch, hkv, d), generator=g, device="cuda").to(dtype)
+            vn = torch.randn((batch, hkv, d), generator=g, device="cuda").to(dtype)
+            check(cache, p.step(q, kn, vn), q)
+        a = p.attend(q)
+        out, lse, sel = a.output.clone(), a.lse.clone(), a.selected_blocks.clone()
+        b = p.attend(q, use_graph=True)
+        torch.cuda.synchronize()
+        assert torch.equal(out, b.output) and torch.equal(lse, b.lse)
+        assert torch.equal(sel, b.selected_blocks)
+        check(cache, b, q)
