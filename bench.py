@@ -29,8 +29,14 @@ Default run (N=1):
   * qwen2_decode: a randomly initialised Qwen2-1.5B-shaped model (cfg4's
                  attention shape) decoding after an 8K MoBA prefill, per-token
                  time eager and as one whole-model hipGraph.
+  * reference_c12_prefill / reference_decode_matrix: the reference's own
+                 published shapes -- C12 prefill fwd+bwd (T 32768, 8 heads,
+                 D 128, chunk 512, top-4) and the P01 / P18 rows of its
+                 decode matrix as prepared graph / eager steps -- with its A40
+                 figures beside them as context only.
   * cpu_baseline: the FP64 CPU oracle (routing + fixed-route fwd + bwd) on 1 of
-                 the 32 heads of cfg3, scaled x32, on this host's cores.
+                 the 32 heads of cfg3, scaled x32, on this host's cores; and
+                 cfg1 measured in full (routing + FP64 forward, 8 heads).
 Prints ONE JSON line on stdout; progress goes to stderr.
 """
 import argparse
@@ -167,6 +173,37 @@ def bench_prefill(steps, warmup, seed):
     del cases
     torch.cuda.empty_cache()
     return out
+
+
+def bench_prefill_case(case, steps, warmup, rounds=3):
+    """Median of per-round medians of per-step stream-event times of one
+    prefill case, with its algorithmic FLOPs and MFMA fraction."""
+    import torch
+    for _ in range(warmup):
+        case.step()
+    rm = []
+    for _ in range(rounds):
+        torch.cuda.synchronize()
+        rm.append(statistics.median(time_steps(case, max(1, steps // rounds))))
+    pairs, flops, _ = case.flops()
+    ms = statistics.median(rm)
+    return {"ms_per_step": ms, "round_medians_ms": rm, "attended_pairs": pairs,
+            "algorithmic_tflop": flops / 1e12, "tflops": flops / ms / 1e9,
+            "mfma_frac": flops / ms / 1e9 / BF16_PEAK_TFLOPS}
+
+
+def bench_c12(steps, warmup, seed):
+    """The reference's published C12 (configs/core12.yaml: T=32768, 8 heads,
+    D=128, chunk 512, top-4, bf16, N(0,1) Q/K/V/dO; 64 chunks, 63 candidates)
+    fwd+bwd through opt_hip.  The A40 figure beside it is context only."""
+    import torch
+    case = PrefillCase("C12", 32768, 8, 8, 128, 512, 4, 1.0, seed + 5)
+    res = bench_prefill_case(case, steps, warmup)
+    res["reference_a40_ms"] = 54.15
+    res["reference_source"] = "docs/profiling_decision.md:7 (A40, opt baseline wall clock)"
+    del case
+    torch.cuda.empty_cache()
+    return res
 
 
 # ------------------------------------------------------------------- decode
@@ -355,6 +392,33 @@ def decode_roofline(res, name):
             "source": f"profiles/decode_{name}_traffic.md"}
 
 
+# Published prepared-decode figures of the reference (A40, seed 701), context
+# only: docs/prepared_decode_20261102.md:61 ("strict" = finite checks on,
+# "trusted" = caller guarantees finite inputs, as the bound-buffer steps here).
+REFERENCE_PREPARED_US = {
+    "P01": {"strict_graph_step_us": 361.0, "trusted_graph_step_us": 161.0},
+    "P18": {"strict_graph_step_us": 582.0},
+}
+
+
+def bench_reference_decode(steps, warmup, seed):
+    """Prepared graph / eager steps at the reference's decode-matrix rows P01
+    (B 1, 2K, D 64, 32q/8kv) and P18 (B 16, 32K, D 128, 32q/8kv): page 16,
+    chunk 128, top-4, bf16, max_seq_len = length + extra as
+    benchmarks/benchmark_decode.py:105-112 builds the step cache (P18's page
+    table is 2049+ entries wide)."""
+    out = {}
+    for name, batch, length, d in (("P01", 1, 2048, 64), ("P18", 16, 32768, 128)):
+        log(f"decode {name} (reference matrix row, graph + eager) ...")
+        r = bench_decode(batch, 32, 8, d, 16, 128, 4, length, length, steps, warmup, "bf16",
+                         seed + 7)
+        r.pop("contexts", None)
+        r["reference_a40"] = REFERENCE_PREPARED_US[name]
+        out[name] = r
+        log(json.dumps(r))
+    return out
+
+
 # -------------------------------------------------------------- CPU baseline
 
 def cpu_baseline(seed):
@@ -380,6 +444,45 @@ def cpu_baseline(seed):
                       f"FP64 fixed-route forward + backward, {sec:.1f} s on {threads} threads"}
 
 
+def cpu_baseline_cfg1(seed):
+    """cfg1 measured in full on the host: canonical routing + FP64
+    fixed-route forward of all 8 heads (T=4096, D=64, chunk 512, topk 3,
+    Q/K/V iid N(0,1) fp32 with bf16 copies), with the same forward on the
+    GPU (opt_hip, bf16) timed beside it."""
+    import torch
+    import moba_hip
+    from oracle import oracle as O
+    T, H, d, C, K = 4096, 8, 64, 512, 3
+    threads = min(len(os.sched_getaffinity(0)), 16)
+    O.set_threads(threads)
+    g = torch.Generator().manual_seed(seed)
+    q, k, v = (torch.randn(T, H, d, generator=g).bfloat16() for _ in range(3))
+    t0 = time.perf_counter()
+    cu_chunk, chunk_batch, filtered = O.calc_chunks([0, T], C)
+    means = O.chunk_means(O.bits16(k), 0, cu_chunk, filtered, C, 0)
+    sel, _ = O.route_prefill(O.bits16(q), 0, means, cu_chunk, chunk_batch, K - 1)
+    O.attention_fwd(*(x.double().numpy() for x in (q, k, v)), cu_chunk, sel)
+    cpu_ms = (time.perf_counter() - t0) * 1e3
+    qg, kg, vg = (x.cuda() for x in (q, k, v))
+    cu = torch.tensor([0, T], dtype=torch.int32, device="cuda")
+    cfg = {"chunk_size": C, "topk": K}
+    with torch.no_grad():
+        for _ in range(3):
+            moba_hip.run_impl("opt_hip", qg, kg, vg, cu, T, cfg)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(11)]
+        ev[0].record()
+        for i in range(10):
+            moba_hip.run_impl("opt_hip", qg, kg, vg, cu, T, cfg)
+            ev[i + 1].record()
+        torch.cuda.synchronize()
+    gpu_ms = statistics.median(ev[i].elapsed_time(ev[i + 1]) for i in range(10))
+    return {"value": cpu_ms, "unit": "ms per cfg1 forward (all 8 heads, measured)",
+            "cores": threads, "kind": "port",
+            "sample": "cfg1 in full: canonical routing + FP64 fixed-route forward, T=4096, 8 heads, "
+                      "D=64, chunk 512, topk 3",
+            "gpu_forward_ms": gpu_ms}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -388,7 +491,7 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode", "cfg4", "cfg5", "qwen2"],
+    ap.add_argument("--only", choices=["prefill", "decode", "cfg4", "cfg5", "qwen2", "reference"],
                     default=None)
     ap.add_argument("--calib-copy", action="store_true",
                     help="first run one 1 GiB device-to-device copy (a known-size kernel that "
@@ -425,6 +528,14 @@ def main():
         dec5 = bench_decode(32, 16, 1, 96, 64, 1024, 8, 1024, 32768, 256, 8, "fp16",
                             args.seed + 2)
         log(json.dumps({k: v for k, v in dec5.items() if k != "contexts"}))
+
+    c12 = ref_dec = None
+    if args.only in (None, "reference"):
+        log("reference C12 prefill fwd+bwd (T 32768, 8 heads, D 128, chunk 512, top-4) ...")
+        c12 = bench_c12(args.steps, args.warmup, args.seed)
+        log(json.dumps(c12))
+        if not args.no_decode:
+            ref_dec = bench_reference_decode(32, 4, args.seed)
 
     qw = None
     if not args.no_decode and args.only in (None, "qwen2"):
@@ -471,9 +582,15 @@ def main():
         out["decode_mqa"] = dec5
     if qw is not None:
         out["qwen2_decode"] = qw
+    if c12 is not None:
+        out["reference_c12_prefill"] = c12
+    if ref_dec is not None:
+        out["reference_decode_matrix"] = ref_dec
     if not args.no_cpu and pre is not None:
         log("cpu baseline (FP64 oracle, 1 of 32 heads) ...")
         out["cpu_baseline"] = cpu_baseline(args.seed)
+        log("cpu baseline cfg1 (FP64 oracle forward, all heads, measured) ...")
+        out["cpu_baseline"]["cfg1_measured"] = cpu_baseline_cfg1(args.seed)
     print(json.dumps(out), flush=True)
 
 

@@ -65,6 +65,9 @@ def _close(actual, expected, dtype, what):
     (16384, 14, 2, 64, 2048, 3, 1.0),               # cfg2: N(0,1)
     (32768, 32, 32, 128, 4096, 3, 128 ** -0.5),     # cfg3: N(0,1) / sqrt(128), as the benchmark config specifies
     (32768, 32, 32, 128, 4096, 3, 1.0),             # cfg3 shape, unscaled (sharper softmax)
+    # the reference's published C12 (configs/core12.yaml: 8 heads, D 128,
+    # chunk 512, top-4, N(0,1)): 64 chunks, 63 candidates per row
+    (32768, 8, 8, 128, 512, 4, 1.0),
 ])
 def test_prefill_full_size(cuda_device, T, hq, hkv, d, chunk, topk, in_scale):
     from moba_hip.ops import prefill as P
