@@ -67,8 +67,9 @@ int moba_hip_route_prefill(const void* q, int dtype, int T, int Hq, int Hkv, int
  * counts[E], row_off[E+1], tile_off[E+1] (tiles of block_rows rows), rows[sum
  * counts] = ((s*Hq + h) << 3) | j where j is the chunk's rank in sel[s,h,:]
  * (R <= 8, T*Hq < 2^28); the partial slot of that row is (s*Hq + h)*R + j.
- * work is an int32 workspace of moba_hip_pack_experts_work(T, Hq, Hkv, F)
- * entries (per-block candidate counts of each expert).
+ * work is an 8-byte aligned int32 workspace of moba_hip_pack_experts_work(T,
+ * Hq, Hkv, F) entries (64-bit selection masks of every (token, head), then
+ * per-block candidate counts of each expert).
  * Replaces the nonzero/index_select packing of grouped_attention.py:78-94. */
 int moba_hip_pack_experts(const int* sel, int T, int Hq, int Hkv, int R,
                           const int* cu_chunk, const int* chunk_batch, const int* cu_seqlens,

@@ -79,9 +79,52 @@ __global__ __launch_bounds__(256) void chunk_means_kernel(const uint16_t* __rest
 }
 
 // One thread per (token, q head): a workgroup takes 256 consecutive tokens of
-// one head, so the means rows read in the candidate loop are the same for the
-// whole wave, and the token's q row is read once into registers.
-template <int DT, int DP>
+// one head.  The means rows its tokens score (filtered indices [flo, fhi) of
+// the head's kv head) go through LDS in tiles of kRouteTile rows.  A wave
+// walks the union of its lanes' candidate ranges in a wave-uniform loop:
+// each 16-lane row of the wave reads 16 values of the candidate's means row
+// into one register per 16 dims, and the fma chain takes dim d from lane
+// d % 16 of its row by a DPP row broadcast (an operand modifier of the fma),
+// so a means row costs DP / 16 LDS reads per wave instead of DP / 4
+// broadcast 16-byte reads; lanes outside a candidate's range discard its
+// score.  The token's q row is held in registers (fp32 up to 128 dims, the
+// input dtype above).  The fma chain of each candidate is the canonical
+// order, unchanged.
+constexpr int kRouteTile = 32;
+
+// acc = fma(lane (row base + j) of m, q[j], acc) for j = 0..15 in order: the
+// fma takes its first operand through a DPP row broadcast (row_newbcast),
+// which the compiler does not fold on its own.  The leading s_nop covers the
+// DPP read-after-VALU-write hazard on m (the compiler does not look inside
+// the block).
+MOBA_DEV float fma16_bcast(float acc, float m, const float* q) {
+  asm volatile(
+      "s_nop 1\n"
+      "v_fmac_f32_dpp %0, %1, %2 row_newbcast:0 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %3 row_newbcast:1 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %4 row_newbcast:2 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %5 row_newbcast:3 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %6 row_newbcast:4 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %7 row_newbcast:5 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %8 row_newbcast:6 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %9 row_newbcast:7 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %10 row_newbcast:8 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %11 row_newbcast:9 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %12 row_newbcast:10 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %13 row_newbcast:11 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %14 row_newbcast:12 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %15 row_newbcast:13 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %16 row_newbcast:14 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %17 row_newbcast:15 row_mask:0xf bank_mask:0xf\n"
+      : "+v"(acc)
+      : "v"(m), "v"(q[0]), "v"(q[1]), "v"(q[2]), "v"(q[3]), "v"(q[4]), "v"(q[5]), "v"(q[6]),
+        "v"(q[7]), "v"(q[8]), "v"(q[9]), "v"(q[10]), "v"(q[11]), "v"(q[12]), "v"(q[13]),
+        "v"(q[14]), "v"(q[15]));
+  return acc;
+}
+
+// DE: the head dim when it is DP exactly (no per-piece bound checks), else 0.
+template <int DT, int DP, int DE>
 __global__ __launch_bounds__(256) void route_kernel(const uint16_t* __restrict__ q, int T, int Hq,
                                                     int Hkv, int D,
                                                     const float* __restrict__ means,
@@ -90,22 +133,48 @@ __global__ __launch_bounds__(256) void route_kernel(const uint16_t* __restrict__
                                                     const int* __restrict__ first_chunk, int R,
                                                     int F, int* __restrict__ sel,
                                                     float* __restrict__ gate) {
-  const int s = blockIdx.x * 256 + threadIdx.x;
+  __shared__ __attribute__((aligned(16))) float mt[kRouteTile * DP];
+  __shared__ int red[2][4];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int s = blockIdx.x * 256 + tid;
   const int h = blockIdx.y;
-  if (s >= T) return;
+  const bool live = s < T;
   const int G = Hq / Hkv, kh = h / G;
-  // chunk containing s
+  // chunk containing s (the last token's for the threads past T)
+  const int sc = live ? s : T - 1;
   int lo = 0, hi = nchunk - 1;
   while (lo < hi) {
     int mid = (lo + hi + 1) >> 1;
-    if (cu_chunk[mid] <= s) lo = mid; else hi = mid - 1;
+    if (cu_chunk[mid] <= sc) lo = mid; else hi = mid - 1;
   }
   const int cs = lo, b = chunk_batch[cs], c0 = first_chunk[cs];
+  // this thread's candidates are filtered rows [c0 - b, cs - b)
+  const int f0 = c0 - b, f1 = cs - b;
+  int mn = live && f1 > f0 ? f0 : 0x7fffffff, mx = live && f1 > f0 ? f1 : 0;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    mn = min(mn, __shfl_xor(mn, o, 64));
+    mx = max(mx, __shfl_xor(mx, o, 64));
+  }
+  const int wlo = __builtin_amdgcn_readfirstlane(mn), whi = __builtin_amdgcn_readfirstlane(mx);
+  if (lane == 0) { red[0][tid >> 6] = wlo; red[1][tid >> 6] = whi; }
+  __syncthreads();
+  const int flo = min(min(red[0][0], red[0][1]), min(red[0][2], red[0][3]));
+  const int fhi = max(max(red[1][0], red[1][1]), max(red[1][2], red[1][3]));
+
   const int64_t idx = (int64_t)s * Hq + h;
   constexpr int NQ = DP / 8;
+  constexpr bool QF32 = DP <= 128;      // q row as fp32 registers
   u16x8_t qv[NQ];
 #pragma unroll
-  for (int i = 0; i < NQ; ++i) qv[i] = i * 8 < D ? ld8(q + idx * D + i * 8) : zero8();
+  for (int i = 0; i < NQ; ++i) qv[i] = (live && i * 8 < D) ? ld8(q + idx * D + i * 8) : zero8();
+  float qf[QF32 ? DP : 1];
+  if constexpr (QF32) {
+#pragma unroll
+    for (int i = 0; i < NQ; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qf[i * 8 + e] = to_f32<DT>(qv[i][e]);
+  }
 
   float val[kMaxRemote];
   int ix[kMaxRemote];
@@ -113,39 +182,65 @@ __global__ __launch_bounds__(256) void route_kernel(const uint16_t* __restrict__
 #pragma unroll
   for (int j = 0; j < kMaxRemote; ++j) { val[j] = -INFINITY; ix[j] = -1; }
 
-  for (int c = c0; c < cs; ++c) {
-    const float* mr = means + ((int64_t)(c - b) * Hkv + kh) * D;
-    // sequential fma chain over d = 0 .. D-1
-    float acc = 0.0f;
+  // LDS tile: rows of DP floats, columns past D zero (so are q's), and
+  // fma(0, 0, acc) == acc keeps the chain exact over the padding
+  constexpr int NST = (kRouteTile * DP / 4 + 255) / 256;
+  constexpr int NM = DP / 16;  // registers of a means row per lane
+  for (int t0 = flo; t0 < fhi; t0 += kRouteTile) {
+    const int nt = min(kRouteTile, fhi - t0);
+    f32x4_t stg[NST];
 #pragma unroll
-    for (int i = 0; i < NQ; ++i) {
-      if (i * 8 >= D) break;
-      const f32x4_t m0 = *reinterpret_cast<const f32x4_t*>(mr + i * 8);
-      const f32x4_t m1 = *reinterpret_cast<const f32x4_t*>(mr + i * 8 + 4);
-      acc = fmaf(m0[0], to_f32<DT>(qv[i][0]), acc);
-      acc = fmaf(m0[1], to_f32<DT>(qv[i][1]), acc);
-      acc = fmaf(m0[2], to_f32<DT>(qv[i][2]), acc);
-      acc = fmaf(m0[3], to_f32<DT>(qv[i][3]), acc);
-      acc = fmaf(m1[0], to_f32<DT>(qv[i][4]), acc);
-      acc = fmaf(m1[1], to_f32<DT>(qv[i][5]), acc);
-      acc = fmaf(m1[2], to_f32<DT>(qv[i][6]), acc);
-      acc = fmaf(m1[3], to_f32<DT>(qv[i][7]), acc);
+    for (int i = 0; i < NST; ++i) {
+      const int x = tid + 256 * i, r = x / (DP / 4), d = (x % (DP / 4)) * 4;
+      stg[i] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+      if (r < nt && d < D)
+        stg[i] = *reinterpret_cast<const f32x4_t*>(means + ((int64_t)(t0 + r) * Hkv + kh) * D + d);
     }
-    if (gate) gate[((int64_t)(c - b) * Hq + h) * T + s] = acc;
-    // stable insertion into the descending list: equal scores stay behind the
-    // earlier (lower) chunk, so exact ties resolve to the lowest index.
-    if (cnt == R && !(acc > val[R - 1])) continue;
-    int pos = 0;
+    __syncthreads();  // the previous tile is consumed
 #pragma unroll
-    for (int j = 0; j < kMaxRemote; ++j) pos += (j < cnt && val[j] >= acc);
+    for (int i = 0; i < NST; ++i) {
+      const int x = tid + 256 * i;
+      if (x < kRouteTile * DP / 4) *reinterpret_cast<f32x4_t*>(mt + x * 4) = stg[i];
+    }
+    __syncthreads();
+    const int fa = max(wlo, t0), fb = min(whi, t0 + nt);
+    for (int f = fa; f < fb; ++f) {
+      const float* mr = mt + (f - t0) * DP + (lane & 15);
+      float mv[NM];
 #pragma unroll
-    for (int j = kMaxRemote - 1; j >= 1; --j)
-      if (j > pos && j < R) { val[j] = val[j - 1]; ix[j] = ix[j - 1]; }
+      for (int i = 0; i < NM; ++i) mv[i] = mr[16 * i];
+      // sequential fma chain over d = 0 .. DP-1 (zero past D)
+      float acc = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kMaxRemote; ++j)
-      if (j == pos) { val[j] = acc; ix[j] = c; }
-    if (cnt < R) cnt++;
+      for (int i = 0; i < NM; ++i) {
+        if constexpr (QF32) {
+          acc = fma16_bcast(acc, mv[i], qf + 16 * i);
+        } else {
+          float qq[16];
+#pragma unroll
+          for (int e = 0; e < 16; ++e) qq[e] = to_f32<DT>(qv[2 * i + e / 8][e % 8]);
+          acc = fma16_bcast(acc, mv[i], qq);
+        }
+      }
+      if (!(live && f >= f0 && f < f1)) continue;
+      const int c = f + b;
+      if (gate) gate[((int64_t)f * Hq + h) * T + s] = acc;
+      // stable insertion into the descending list: equal scores stay behind the
+      // earlier (lower) chunk, so exact ties resolve to the lowest index.
+      if (cnt == R && !(acc > val[R - 1])) continue;
+      int pos = 0;
+#pragma unroll
+      for (int j = 0; j < kMaxRemote; ++j) pos += (j < cnt && val[j] >= acc);
+#pragma unroll
+      for (int j = kMaxRemote - 1; j >= 1; --j)
+        if (j > pos && j < R) { val[j] = val[j - 1]; ix[j] = ix[j - 1]; }
+#pragma unroll
+      for (int j = 0; j < kMaxRemote; ++j)
+        if (j == pos) { val[j] = acc; ix[j] = c; }
+      if (cnt < R) cnt++;
+    }
   }
+  if (!live) return;
   // ascending chunk order for the slot list (static sorting network)
 #pragma unroll
   for (int pass = 0; pass < kMaxRemote; ++pass) {
@@ -169,13 +264,33 @@ __global__ void fill_f32_kernel(float* p, int64_t n, float v) {
 // sequence end, enumerated g-major like the reference's nonzero over
 // [F*Hkv, G*T] (grouped_attention.py:78-80).
 
-MOBA_DEV int find_slot(const int* __restrict__ sel, int64_t row, int R, int c) {
-  const int* p = sel + row * R;
-  for (int j = 0; j < R; ++j) if (p[j] == c) return j;
-  return -1;
+// Selection bitmasks: word w of row (s, h) has bit f % 64 set when (s, h)
+// selected the chunk of filtered index f, f / 64 == w; laid out
+// mask[(h * NW + w) * T + s], so the candidate scans of the experts, which
+// walk s for a fixed (h, w), read 8 consecutive bytes per candidate instead
+// of a strided R-int row of sel.  One thread per (s, h).
+__global__ __launch_bounds__(256) void sel_mask_kernel(const int* __restrict__ sel, int T, int Hq,
+                                                       int R, const int* __restrict__ chunk_batch,
+                                                       int NW, uint64_t* __restrict__ mask) {
+  const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;  // s * Hq + h
+  if (row >= (int64_t)T * Hq) return;
+  const int s = (int)(row / Hq), h = (int)(row % Hq);
+  int fs[kMaxRemote];
+#pragma unroll
+  for (int j = 0; j < kMaxRemote; ++j) {
+    const int c = j < R ? sel[row * R + j] : -1;
+    fs[j] = c >= 0 ? c - chunk_batch[c] : -1;
+  }
+  for (int w = 0; w < NW; ++w) {
+    uint64_t m = 0;
+#pragma unroll
+    for (int j = 0; j < kMaxRemote; ++j)
+      if (fs[j] >= 0 && (fs[j] >> 6) == w) m |= 1ull << (fs[j] & 63);
+    mask[((int64_t)h * NW + w) * T + s] = m;
+  }
 }
 
-struct ExpertRange { int c, kh, s0, ns, G; };
+struct ExpertRange { int c, f, kh, s0, ns, G; };
 
 MOBA_DEV ExpertRange expert_range(int e, int Hq, int Hkv, const int* cu_chunk,
                                   const int* chunk_batch, const int* cu_seqlens,
@@ -183,6 +298,7 @@ MOBA_DEV ExpertRange expert_range(int e, int Hq, int Hkv, const int* cu_chunk,
   ExpertRange r;
   const int f = e / Hkv;
   r.kh = e % Hkv;
+  r.f = f;
   r.c = filtered[f];
   r.s0 = cu_chunk[r.c + 1];
   r.ns = cu_seqlens[chunk_batch[r.c] + 1] - r.s0;
@@ -197,17 +313,19 @@ MOBA_DEV ExpertRange expert_range(int e, int Hq, int Hkv, const int* cu_chunk,
 constexpr int kCandBlock = 2048;
 
 __global__ __launch_bounds__(256) void expert_count_kernel(
-    const int* __restrict__ sel, int Hq, int Hkv, int R, const int* __restrict__ cu_chunk,
-    const int* __restrict__ chunk_batch, const int* __restrict__ cu_seqlens,
-    const int* __restrict__ filtered, int nbmax, int* __restrict__ work) {
+    const uint64_t* __restrict__ mask, int T, int NW, int Hq, int Hkv,
+    const int* __restrict__ cu_chunk, const int* __restrict__ chunk_batch,
+    const int* __restrict__ cu_seqlens, const int* __restrict__ filtered, int nbmax,
+    int* __restrict__ work) {
   const int e = blockIdx.x, b = blockIdx.y;
   ExpertRange x = expert_range(e, Hq, Hkv, cu_chunk, chunk_batch, cu_seqlens, filtered);
   const int64_t n = (int64_t)x.G * x.ns;
   const int64_t i1 = min(n, (int64_t)(b + 1) * kCandBlock);
+  const int mw = x.f >> 6, bit = x.f & 63;
   int cnt = 0;
   for (int64_t i = (int64_t)b * kCandBlock + threadIdx.x; i < i1; i += 256) {
     const int g = (int)(i / x.ns), s = x.s0 + (int)(i % x.ns);
-    cnt += find_slot(sel, (int64_t)s * Hq + x.kh * x.G + g, R, x.c) >= 0;
+    cnt += (int)((mask[((int64_t)(x.kh * x.G + g) * NW + mw) * T + s] >> bit) & 1);
   }
   __shared__ int part[4];
 #pragma unroll
@@ -259,12 +377,14 @@ __global__ __launch_bounds__(1024) void expert_scan_kernel(int* __restrict__ wor
 
 // Ordered compaction: rows[row_off[e] + rank] = ((s*Hq + h) << 3) | j (R <= 8).
 __global__ __launch_bounds__(256) void expert_fill_kernel(
-    const int* __restrict__ sel, int Hq, int Hkv, int R, const int* __restrict__ cu_chunk,
-    const int* __restrict__ chunk_batch, const int* __restrict__ cu_seqlens,
-    const int* __restrict__ filtered, const int* __restrict__ row_off, int nbmax,
-    const int* __restrict__ work, int* __restrict__ rows) {
+    const uint64_t* __restrict__ mask, int T, int NW, int Hq, int Hkv,
+    const int* __restrict__ cu_chunk, const int* __restrict__ chunk_batch,
+    const int* __restrict__ cu_seqlens, const int* __restrict__ filtered,
+    const int* __restrict__ row_off, int nbmax, const int* __restrict__ work,
+    int* __restrict__ rows) {
   const int e = blockIdx.x, b = blockIdx.y;
   ExpertRange x = expert_range(e, Hq, Hkv, cu_chunk, chunk_batch, cu_seqlens, filtered);
+  const int mw = x.f >> 6, bit = x.f & 63;
   const int64_t n = (int64_t)x.G * x.ns;
   const int64_t i0 = (int64_t)b * kCandBlock, i1 = min(n, i0 + kCandBlock);
   if (i0 >= i1) return;
@@ -278,11 +398,17 @@ __global__ __launch_bounds__(256) void expert_fill_kernel(
       const int g = (int)(i / x.ns);
       s = x.s0 + (int)(i % x.ns);
       h = x.kh * x.G + g;
-      slot = find_slot(sel, (int64_t)s * Hq + h, R, x.c);
+      const uint64_t* mh = mask + (int64_t)h * NW * T + s;
+      const uint64_t m = mh[(int64_t)mw * T];
+      if ((m >> bit) & 1) {
+        // slot = the selected chunks before this one (sel is ascending)
+        slot = __popcll(m & ((1ull << bit) - 1ull));
+        for (int w2 = 0; w2 < mw; ++w2) slot += __popcll(mh[(int64_t)w2 * T]);
+      }
     }
-    const uint64_t mask = __ballot(slot >= 0);
-    const int before = __popcll(mask & ((1ull << lane) - 1ull));
-    if (lane == 0) wtot[w] = __popcll(mask);
+    const uint64_t hits = __ballot(slot >= 0);
+    const int before = __popcll(hits & ((1ull << lane) - 1ull));
+    if (lane == 0) wtot[w] = __popcll(hits);
     __syncthreads();
     int off = out;
     for (int k2 = 0; k2 < w; ++k2) off += wtot[k2];
@@ -342,21 +468,30 @@ extern "C" int moba_hip_route_prefill(const void* q, int dtype, int T, int Hq, i
   if (D > 256) { moba_set_error("route_prefill: head_dim must be at most 256"); return MOBA_ERR_ARG; }
   dim3 grid((unsigned)((T + 255) / 256), (unsigned)Hq), block(256);
   const uint16_t* qp = (const uint16_t*)q;
-#define MOBA_ROUTE(DT_, DP_) \
-  hipLaunchKernelGGL((route_kernel<DT_, DP_>), grid, block, 0, st, qp, T, Hq, Hkv, D, means, \
+#define MOBA_ROUTE(DT_, DP_, DE_) \
+  hipLaunchKernelGGL((route_kernel<DT_, DP_, DE_>), grid, block, 0, st, qp, T, Hq, Hkv, D, means, \
                      cu_chunk, nchunk, chunk_batch, first_chunk, R, F, sel, gate)
+#define MOBA_ROUTE_DT(DT_) \
+  if (D == 64) MOBA_ROUTE(DT_, 64, 64); else if (D < 64) MOBA_ROUTE(DT_, 64, 0); \
+  else if (D == 128) MOBA_ROUTE(DT_, 128, 128); else if (D < 128) MOBA_ROUTE(DT_, 128, 0); \
+  else if (D == 256) MOBA_ROUTE(DT_, 256, 256); else MOBA_ROUTE(DT_, 256, 0);
   if (dtype == 0) {
-    if (D <= 64) MOBA_ROUTE(0, 64); else if (D <= 128) MOBA_ROUTE(0, 128); else MOBA_ROUTE(0, 256);
+    MOBA_ROUTE_DT(0)
   } else {
-    if (D <= 64) MOBA_ROUTE(1, 64); else if (D <= 128) MOBA_ROUTE(1, 128); else MOBA_ROUTE(1, 256);
+    MOBA_ROUTE_DT(1)
   }
+#undef MOBA_ROUTE_DT
 #undef MOBA_ROUTE
   return moba_launch_status("route_prefill");
 }
 
+// Work ints of moba_hip_pack_experts: the selection bitmasks (2 ints per
+// 64-bit word), then the per-(expert, block) counts.
+int64_t mask_ints(int T, int Hq, int F) { return (int64_t)T * Hq * ((F + 63) / 64) * 2; }
+
 extern "C" int64_t moba_hip_pack_experts_work(int T, int Hq, int Hkv, int F) {
   if (T < 0 || Hq < 1 || Hkv < 1 || Hq % Hkv || F < 0) return -1;
-  return (int64_t)F * Hkv * expert_blocks(T, Hq, Hkv);
+  return mask_ints(T, Hq, F) + (int64_t)F * Hkv * expert_blocks(T, Hq, Hkv);
 }
 
 extern "C" int moba_hip_pack_experts(const int* sel, int T, int Hq, int Hkv, int R,
@@ -368,16 +503,21 @@ extern "C" int moba_hip_pack_experts(const int* sel, int T, int Hq, int Hkv, int
   if ((int64_t)T * Hq * R >= (1ll << 31) || (int64_t)T * Hq >= (1ll << 28)) { moba_set_error("pack_experts: T*Hq*R exceeds int32 or T*Hq exceeds 2^28"); return MOBA_ERR_ARG; }
   if (R > 8) { moba_set_error("pack_experts: at most 8 remote chunks per query"); return MOBA_ERR_ARG; }
   if (Hkv < 1 || Hq % Hkv) { moba_set_error("pack_experts: Hq must be a multiple of Hkv"); return MOBA_ERR_ARG; }
-  if (work == nullptr) { moba_set_error("pack_experts: the work buffer (moba_hip_pack_experts_work ints) is required"); return MOBA_ERR_ARG; }
+  if (work == nullptr || ((uintptr_t)work & 7)) { moba_set_error("pack_experts: the work buffer (moba_hip_pack_experts_work ints, 8-byte aligned) is required"); return MOBA_ERR_ARG; }
   hipStream_t st = (hipStream_t)stream;
   const int E = F * Hkv;
   const int nbmax = (int)expert_blocks(T, Hq, Hkv);
   if (nbmax < 1) return MOBA_OK;
-  hipLaunchKernelGGL(expert_count_kernel, dim3(E, nbmax), dim3(256), 0, st, sel, Hq, Hkv, R,
-                     cu_chunk, chunk_batch, cu_seqlens, filtered, nbmax, work);
-  hipLaunchKernelGGL(expert_scan_kernel, dim3(1), dim3(1024), 0, st, work, nbmax, E, block_rows,
+  const int NW = (F + 63) / 64;
+  uint64_t* mask = reinterpret_cast<uint64_t*>(work);  // 8-byte aligned: the work buffer's start
+  int* cwork = work + mask_ints(T, Hq, F);
+  hipLaunchKernelGGL(sel_mask_kernel, dim3((unsigned)(((int64_t)T * Hq + 255) / 256)), dim3(256),
+                     0, st, sel, T, Hq, R, chunk_batch, NW, mask);
+  hipLaunchKernelGGL(expert_count_kernel, dim3(E, nbmax), dim3(256), 0, st, mask, T, NW, Hq, Hkv,
+                     cu_chunk, chunk_batch, cu_seqlens, filtered, nbmax, cwork);
+  hipLaunchKernelGGL(expert_scan_kernel, dim3(1), dim3(1024), 0, st, cwork, nbmax, E, block_rows,
                      counts, row_off, tile_off);
-  hipLaunchKernelGGL(expert_fill_kernel, dim3(E, nbmax), dim3(256), 0, st, sel, Hq, Hkv, R,
-                     cu_chunk, chunk_batch, cu_seqlens, filtered, row_off, nbmax, work, rows);
+  hipLaunchKernelGGL(expert_fill_kernel, dim3(E, nbmax), dim3(256), 0, st, mask, T, NW, Hq, Hkv,
+                     cu_chunk, chunk_batch, cu_seqlens, filtered, row_off, nbmax, cwork, rows);
   return moba_launch_status("pack_experts");
 }

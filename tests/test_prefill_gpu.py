@@ -46,6 +46,8 @@ def _gpu_route(q, k, cu, cfg, precision=0):
     # many candidate blocks of 2048 per expert (multi-workgroup compaction)
     (14, 2, 64, (12000, 3000), 512, 4),
     (8, 8, 128, (4100,), 512, 3),
+    # more than 64 candidate chunks: selection masks of several 64-bit words
+    (4, 2, 64, (3000, 1500), 16, 4),
 ])
 def test_routing_bit_exact(cuda_device, hq, hkv, dim, lens, chunk, topk, dtype, precision):
     q, k, v, cu, ml, _ = prefill_inputs(hq, hkv, dim, lens, dtype, seed=7)
