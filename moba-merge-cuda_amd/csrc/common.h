@@ -300,6 +300,86 @@ MOBA_DEV float wave_sum(float v) {
   return v;
 }
 
+
+// acc = fma(b_j, m[j], acc) for j = 0..7 in order, b_j = lane (row base + J0
+// + j) of b: the fma reads b through a DPP row broadcast (row_newbcast, one
+// source lane for each 16-lane row), which the compiler does not form on its
+// own.  A 16-lane row then holds 16 dims of a row vector in one register, and
+// a whole wave streams a sequential fma chain against it with no LDS reads.
+// The leading s_nop covers the DPP read-after-VALU-write hazard on b (the
+// compiler does not look inside the block).
+template <int J0>
+MOBA_DEV float fma8_bcast(float acc, float b, const float (&m)[8]) {
+  static_assert(J0 == 0 || J0 == 8, "row lanes 0..7 or 8..15");
+  if constexpr (J0 == 0) {
+    asm volatile(
+        "s_nop 1\n"
+        "v_fmac_f32_dpp %0, %1, %2 row_newbcast:0 row_mask:0xf bank_mask:0xf\n"
+        "v_fmac_f32_dpp %0, %1, %3 row_newbcast:1 row_mask:0xf bank_mask:0xf\n"
+        "v_fmac_f32_dpp %0, %1, %4 row_newbcast:2 row_mask:0xf bank_mask:0xf\n"
+        "v_fmac_f32_dpp %0, %1, %5 row_newbcast:3 row_mask:0xf bank_mask:0xf\n"
+        "v_fmac_f32_dpp %0, %1, %6 row_newbcast:4 row_mask:0xf bank_mask:0xf\n"
+        "v_fmac_f32_dpp %0, %1, %7 row_newbcast:5 row_mask:0xf bank_mask:0xf\n"
+        "v_fmac_f32_dpp %0, %1, %8 row_newbcast:6 row_mask:0xf bank_mask:0xf\n"
+        "v_fmac_f32_dpp %0, %1, %9 row_newbcast:7 row_mask:0xf bank_mask:0xf\n"
+        : "+v"(acc)
+        : "v"(b), "v"(m[0]), "v"(m[1]), "v"(m[2]), "v"(m[3]), "v"(m[4]), "v"(m[5]), "v"(m[6]),
+          "v"(m[7]));
+  } else {
+    asm volatile(
+        "s_nop 1\n"
+        "v_fmac_f32_dpp %0, %1, %2 row_newbcast:8 row_mask:0xf bank_mask:0xf\n"
+        "v_fmac_f32_dpp %0, %1, %3 row_newbcast:9 row_mask:0xf bank_mask:0xf\n"
+        "v_fmac_f32_dpp %0, %1, %4 row_newbcast:10 row_mask:0xf bank_mask:0xf\n"
+        "v_fmac_f32_dpp %0, %1, %5 row_newbcast:11 row_mask:0xf bank_mask:0xf\n"
+        "v_fmac_f32_dpp %0, %1, %6 row_newbcast:12 row_mask:0xf bank_mask:0xf\n"
+        "v_fmac_f32_dpp %0, %1, %7 row_newbcast:13 row_mask:0xf bank_mask:0xf\n"
+        "v_fmac_f32_dpp %0, %1, %8 row_newbcast:14 row_mask:0xf bank_mask:0xf\n"
+        "v_fmac_f32_dpp %0, %1, %9 row_newbcast:15 row_mask:0xf bank_mask:0xf\n"
+        : "+v"(acc)
+        : "v"(b), "v"(m[0]), "v"(m[1]), "v"(m[2]), "v"(m[3]), "v"(m[4]), "v"(m[5]), "v"(m[6]),
+          "v"(m[7]));
+  }
+  return acc;
+}
+
+// Four chains interleaved: acc[k] = fma(lane (row base + J0 + j) of b[k],
+// m[j], acc[k]) for j = 0..7 in order, chain k independent of the others (so
+// consecutive instructions do not wait on each other).  Hazard as above.
+#define MOBA_F4(J, MJ)                                                                         \
+  "v_fmac_f32_dpp %0, %4, " MJ " row_newbcast:" #J " row_mask:0xf bank_mask:0xf\n"             \
+  "v_fmac_f32_dpp %1, %5, " MJ " row_newbcast:" #J " row_mask:0xf bank_mask:0xf\n"             \
+  "v_fmac_f32_dpp %2, %6, " MJ " row_newbcast:" #J " row_mask:0xf bank_mask:0xf\n"             \
+  "v_fmac_f32_dpp %3, %7, " MJ " row_newbcast:" #J " row_mask:0xf bank_mask:0xf\n"
+template <int J0>
+MOBA_DEV void fma8_bcast4(float (&acc)[4], const float (&b)[4], const float (&m)[8]) {
+  static_assert(J0 == 0 || J0 == 8, "row lanes 0..7 or 8..15");
+  if constexpr (J0 == 0) {
+    asm volatile("s_nop 1\n" MOBA_F4(0, "%8") MOBA_F4(1, "%9") MOBA_F4(2, "%10") MOBA_F4(3, "%11")
+                 MOBA_F4(4, "%12") MOBA_F4(5, "%13") MOBA_F4(6, "%14") MOBA_F4(7, "%15")
+                 : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3])
+                 : "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]), "v"(m[0]), "v"(m[1]), "v"(m[2]),
+                   "v"(m[3]), "v"(m[4]), "v"(m[5]), "v"(m[6]), "v"(m[7]));
+  } else {
+    asm volatile("s_nop 1\n" MOBA_F4(8, "%8") MOBA_F4(9, "%9") MOBA_F4(10, "%10") MOBA_F4(11, "%11")
+                 MOBA_F4(12, "%12") MOBA_F4(13, "%13") MOBA_F4(14, "%14") MOBA_F4(15, "%15")
+                 : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3])
+                 : "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]), "v"(m[0]), "v"(m[1]), "v"(m[2]),
+                   "v"(m[3]), "v"(m[4]), "v"(m[5]), "v"(m[6]), "v"(m[7]));
+  }
+}
+#undef MOBA_F4
+
+// Order-preserving 64-bit key of a route score: larger key = higher score,
+// then lower chunk (the stable top-k order); 0 for -inf / NaN, which are never
+// selected.  -0 and +0 compare equal, as the float comparison does.
+MOBA_DEV uint64_t route_key(float v, int c) {
+  if (!(v > -INFINITY)) return 0;
+  uint32_t u = __float_as_uint(v + 0.0f);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)u << 32) | (uint32_t)(0x7fffffff - c);
+}
+
 }  // namespace moba
 
 // Error reporting shared by the C-ABI entry points.

@@ -71,6 +71,7 @@ constexpr int kFwNarrow = 8;
 constexpr int kFwWide = 12;
 constexpr int kWideBlocksPerWorkgroup = 16;  // expected blocks at which 12 waves pay
 constexpr int kMaxSlots = 9;    // current chunk + up to 8 routed chunks
+constexpr int kMaxSeg = 64;     // 64-chunk segments of the parallel union (more: one wave)
 constexpr int kGroupMax = 16;   // q heads of one (virtual) kv-head group: the MFMA's 16 columns
 constexpr size_t kDynMax = 64 * 1024;  // dynamic LDS of one launch (route scratch + table row)
 
@@ -121,7 +122,9 @@ constexpr size_t fused_static_lds(int DP, int FW) {
 }
 constexpr size_t kLdsBytes = 160 * 1024;
 
-template <int DT, int DP, int FW>
+// WROUTE: the launch has rows with more than 64 closed chunks (the wide
+// score and top-k forms below are compiled in only then).
+template <int DT, int DP, int FW, bool WROUTE>
 __global__ __launch_bounds__(64 * FW) void fused_kernel(FusedArgs a) {
   constexpr int kFW = FW;
   constexpr int NKS = DP / 32;  // 32-d k-steps of S^T
@@ -139,6 +142,7 @@ __global__ __launch_bounds__(64 * FW) void fused_kernel(FusedArgs a) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[STAGE_BYTES > MERGE_BYTES ? STAGE_BYTES : MERGE_BYTES];
   extern __shared__ int dyn[];
   __shared__ int s_info[8];
+  __shared__ int s_segn[kMaxSeg], s_segb[kMaxSeg];  // per 64-chunk segment: items, blocks
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g4 = lane >> 4, c16 = lane & 15;
   int split, S, rowk;
@@ -313,45 +317,139 @@ __global__ __launch_bounds__(64 * FW) void fused_kernel(FusedArgs a) {
   for (int c = tid; c <= cur; c += 64 * kFW) umask[c] = (a.dense || c == cur) ? all_heads : 0;
   for (int x = tid; x < G * S1; x += 64 * kFW) sel_s[x] = x % S1 == 0 ? cur : -1;
   if (!a.dense) {
-    // Scores: thread x takes (head x / nc, chunk x % nc) of the tile; each
-    // score is the sequential fp32 fma chain over d of the staged mean row
-    // and the head's q row (fp32 in LDS).
-    for (int c0 = 0; c0 < legal; c0 += 64) {
-      const int nc = min(64, legal - c0);
-      if (c0 > 0) {  // the first 64 means rows came with the first burst
-        load_means(c0, nc, stg);
-        __syncthreads();  // the previous tile's scores are done
-        store_means(stg);
-        __syncthreads();
-      }
-      for (int x = tid; x < G * nc; x += 64 * kFW) {
-        const int g = x / nc, cl = x % nc;
-        const float* qg = qsf + g * DP;
-        const uint16_t* mr = ms + cl * MS;
-        float acc = 0.0f;
-        // operands of 8 pieces (64 d) are read in one batch, then the chain
-        // runs on registers; pieces past D are zero in both rows, and
-        // fma(0, 0, acc) == acc
-        constexpr int JB = RC % 8 == 0 ? 8 : RC % 6 == 0 ? 6 : RC;  // divides RC
+    if constexpr (WROUTE) {
+      // Scores: each is the sequential fp32 fma chain over d of a staged means
+      // row (64 rows per tile) and the head's q row (fp32 in LDS).  Wide routes
+      // (more than 64 closed chunks) stream the means rows with lanes as chunks;
+      // narrow ones take one (head, chunk) item per thread.  The next tile's
+      // means rows are loaded into registers while a tile is scored.
+      const bool wide = legal > 64;
+      for (int c0 = 0; c0 < legal; c0 += 64) {
+        const int nc = min(64, legal - c0);
+        // the first 64 rows came with the first burst; the wide form reads all
+        // of its rows itself in the first pass
+        if (wide && c0 > 0) break;
+        const bool more = !wide && c0 + 64 < legal;
+        if (more) load_means(c0 + 64, min(64, legal - c0 - 64), stg);
+        if (wide) {
+          // unit u = (tile u / nq, heads hpu (u % nq) .. + hpu - 1), nq =
+          // ceil(G / hpu), dealt to the waves, its head chains interleaved.
+          // lane = chunk.  The lane's means
+          // row comes from global memory (L2) into registers and feeds the
+          // unit's head chains; head g's q row sits 16 dims per register, dim
+          // 16 i + j in lane j of each 16-lane row, and reaches the chain by DPP
+          // row broadcast.  Lanes past the closed chunks compute on a clamped
+          // row and store nothing.  (All tiles are scored in the first pass.)
+          if (c0 == 0) {
+            const int ntile = (legal + 63) / 64;
+            const int hpu = 4;  // four interleaved chains (two were slower at G = 4)
+            const int nq = (G + hpu - 1) / hpu;
+            for (int u = w; u < ntile * nq; u += kFW) {
+              const int t0 = (u / nq) * 64, g0 = (u % nq) * hpu;
+              const int c = min(t0 + lane, legal - 1);
+              const uint16_t* mrow = a.means + (((int64_t)sid * a.max_chunks + c) * a.Hkv + kh) * D;
+              u16x8_t mv[RC];
 #pragma unroll
-        for (int j0 = 0; j0 < RC; j0 += JB) {
-          u16x8_t mv[JB];
-          f32x4_t qa[JB], qb[JB];
+              for (int j = 0; j < RC; ++j) mv[j] = j * 8 < D ? ld8(mrow + j * 8) : zero8();
+              float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int j = 0; j < JB; ++j) {
-            mv[j] = ld8(mr + (j0 + j) * 8);
-            qa[j] = *reinterpret_cast<const f32x4_t*>(qg + (j0 + j) * 8);
-            qb[j] = *reinterpret_cast<const f32x4_t*>(qg + (j0 + j) * 8 + 4);
+              for (int i = 0; i < DP / 16; ++i) {
+                float qb[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) qb[k] = qsf[min(g0 + k, G - 1) * DP + 16 * i + c16];
+#pragma unroll
+                for (int hlf = 0; hlf < 2; ++hlf) {
+                  float m[8];
+#pragma unroll
+                  for (int e = 0; e < 8; ++e) m[e] = to_f32<DT>(mv[2 * i + hlf][e]);
+                  if (hlf == 0) fma8_bcast4<0>(acc, qb, m); else fma8_bcast4<8>(acc, qb, m);
+                }
+              }
+              if (t0 + lane < legal) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                  if (k < hpu && g0 + k < G) sc[(g0 + k) * width + t0 + lane] = acc[k];
+              }
+            }
           }
+        } else {
+          for (int x = tid; x < G * nc; x += 64 * kFW) {
+            const int g = x / nc, cl = x % nc;
+            const float* qg = qsf + g * DP;
+            const uint16_t* mr = ms + cl * MS;
+            float acc = 0.0f;
+            // operands of 8 pieces (64 d) are read in one batch, then the chain
+            // runs on registers; pieces past D are zero in both rows, and
+            // fma(0, 0, acc) == acc
+            constexpr int JB = RC % 8 == 0 ? 8 : RC % 6 == 0 ? 6 : RC;  // divides RC
 #pragma unroll
-          for (int j = 0; j < JB; ++j) {
+            for (int j0 = 0; j0 < RC; j0 += JB) {
+              u16x8_t mv[JB];
+              f32x4_t qa[JB], qb[JB];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) acc = fmaf(to_f32<DT>(mv[j][e]), qa[j][e], acc);
+              for (int j = 0; j < JB; ++j) {
+                mv[j] = ld8(mr + (j0 + j) * 8);
+                qa[j] = *reinterpret_cast<const f32x4_t*>(qg + (j0 + j) * 8);
+                qb[j] = *reinterpret_cast<const f32x4_t*>(qg + (j0 + j) * 8 + 4);
+              }
 #pragma unroll
-            for (int e = 0; e < 4; ++e) acc = fmaf(to_f32<DT>(mv[j][4 + e]), qb[j][e], acc);
+              for (int j = 0; j < JB; ++j) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc = fmaf(to_f32<DT>(mv[j][e]), qa[j][e], acc);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc = fmaf(to_f32<DT>(mv[j][4 + e]), qb[j][e], acc);
+              }
+            }
+            sc[g * width + c0 + cl] = acc;
           }
         }
-        sc[g * width + c0 + cl] = acc;
+        if (more) {
+          __syncthreads();  // this tile's scores are done
+          store_means(stg);
+          __syncthreads();
+        }
+      }
+    } else {
+      // Scores: thread x takes (head x / nc, chunk x % nc) of the tile; each
+      // score is the sequential fp32 fma chain over d of the staged mean row
+      // and the head's q row (fp32 in LDS).
+      for (int c0 = 0; c0 < legal; c0 += 64) {
+        const int nc = min(64, legal - c0);
+        if (c0 > 0) {  // the first 64 means rows came with the first burst
+          load_means(c0, nc, stg);
+          __syncthreads();  // the previous tile's scores are done
+          store_means(stg);
+          __syncthreads();
+        }
+        for (int x = tid; x < G * nc; x += 64 * kFW) {
+          const int g = x / nc, cl = x % nc;
+          const float* qg = qsf + g * DP;
+          const uint16_t* mr = ms + cl * MS;
+          float acc = 0.0f;
+          // operands of 8 pieces (64 d) are read in one batch, then the chain
+          // runs on registers; pieces past D are zero in both rows, and
+          // fma(0, 0, acc) == acc
+          constexpr int JB = RC % 8 == 0 ? 8 : RC % 6 == 0 ? 6 : RC;  // divides RC
+#pragma unroll
+          for (int j0 = 0; j0 < RC; j0 += JB) {
+            u16x8_t mv[JB];
+            f32x4_t qa[JB], qb[JB];
+#pragma unroll
+            for (int j = 0; j < JB; ++j) {
+              mv[j] = ld8(mr + (j0 + j) * 8);
+              qa[j] = *reinterpret_cast<const f32x4_t*>(qg + (j0 + j) * 8);
+              qb[j] = *reinterpret_cast<const f32x4_t*>(qg + (j0 + j) * 8 + 4);
+            }
+#pragma unroll
+            for (int j = 0; j < JB; ++j) {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) acc = fmaf(to_f32<DT>(mv[j][e]), qa[j][e], acc);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) acc = fmaf(to_f32<DT>(mv[j][4 + e]), qb[j][e], acc);
+            }
+          }
+          sc[g * width + c0 + cl] = acc;
+        }
       }
     }
     __syncthreads();
@@ -360,6 +458,50 @@ __global__ __launch_bounds__(64 * FW) void fused_kernel(FusedArgs a) {
     // counts the chunks ahead of it in (score desc, chunk asc) order; -inf
     // and NaN scores are never selected.  Same picks as R rounds of "best
     // candidate strictly after the previous pick".
+    //
+    // Wide routes (more than 64 closed chunks; counting ranks costs G x
+    // legal^2 comparisons): wave w takes heads w, w + kFW, ...; each lane
+    // keeps the best R of its chunks (lane, lane + 64, ...) as order keys
+    // (score desc, chunk asc), then R rounds of a wave-wide maximum pick the
+    // head's chunks in rank order -- the same picks.
+    if (WROUTE && legal > 64) {
+      for (int g = w; g < G; g += kFW) {
+        const float* sg = sc + g * width;
+        uint64_t bk[kMaxSlots - 1];
+#pragma unroll
+        for (int r = 0; r < kMaxSlots - 1; ++r) bk[r] = 0;
+        for (int c = lane; c < legal; c += 64) {
+          uint64_t x = route_key(sg[c], c);
+#pragma unroll
+          for (int r = 0; r < kMaxSlots - 1; ++r) {  // insertion into the descending list
+            const uint64_t hi = bk[r] > x ? bk[r] : x, lo = bk[r] > x ? x : bk[r];
+            bk[r] = hi;
+            x = lo;
+          }
+        }
+        for (int r = 0; r < a.R; ++r) {
+          uint64_t m = bk[0];
+#pragma unroll
+          for (int o = 32; o >= 1; o >>= 1) {
+            const uint32_t yl = __shfl_xor((uint32_t)m, o, 64);
+            const uint32_t yh = __shfl_xor((uint32_t)(m >> 32), o, 64);
+            const uint64_t y = ((uint64_t)yh << 32) | yl;
+            m = m > y ? m : y;
+          }
+          if (m == 0) break;  // no selectable chunk left
+          if (bk[0] == m) {   // the one lane holding it (keys are distinct)
+#pragma unroll
+            for (int q2 = 0; q2 < kMaxSlots - 2; ++q2) bk[q2] = bk[q2 + 1];
+            bk[kMaxSlots - 2] = 0;
+          }
+          if (lane == 0) {
+            const int c = 0x7fffffff - (int)(uint32_t)m;
+            sel_s[g * S1 + 1 + r] = c;
+            atomicOr(&umask[c], 1 << g);
+          }
+        }
+      }
+    } else
     for (int x = tid; x < G * legal; x += 64 * kFW) {
       const int g = x / legal, c = x % legal;
       const float* sg = sc + g * width;
@@ -404,36 +546,100 @@ __global__ __launch_bounds__(64 * FW) void fused_kernel(FusedArgs a) {
       a.selected[((int64_t)qrow * a.Hq + hb + g) * S1 + j] = sel_s[x];
     }
   }
-  // items: the union's chunks in ascending order with their head masks, and
-  // the prefix count of 32-token blocks
-  if (w == 0) {
-    int n = 0, nb = 0;
-    for (int c0 = 0; c0 <= cur; c0 += 64) {
-      const int c = c0 + lane;
+  if constexpr (WROUTE) {
+    // items: the union's chunks in ascending order with their head masks, and
+    // the prefix count of 32-token blocks.  Chunks go in segments of 64, one
+    // lane each: with one segment, wave 0 does it; with several, the waves
+    // count their segments' items and blocks, then place them after the counts
+    // of the segments before.
+    const int nseg = cur / 64 + 1;
+    auto seg_items = [&](int sg, int n0, int nb0, bool place, int& cnt, int& nblk) {
+      const int c = sg * 64 + lane;
       const int m = c <= cur ? umask[c] : 0;
       const uint64_t bal = __ballot(m != 0);
-      const int rank = n + __popcll(bal & ((1ull << lane) - 1ull));
       const int ntok = c < cur ? C : p + 1 - cur * C;
-      int blocks = m != 0 ? (ntok + 31) / 32 : 0;
-      // inclusive scan of the block counts over the wave
-      int incl = blocks;
+      const int blocks = m != 0 ? (ntok + 31) / 32 : 0;
+      int incl = blocks;  // inclusive scan of the block counts over the wave
 #pragma unroll
       for (int off = 1; off < 64; off <<= 1) {
         const int y = __shfl_up(incl, off, 64);
         if (lane >= off) incl += y;
       }
-      if (m != 0) {
+      if (place && m != 0) {
+        const int rank = n0 + __popcll(bal & ((1ull << lane) - 1ull));
         item_c[rank] = c;
         item_m[rank] = m;
-        bp[rank] = nb + incl - blocks;
+        bp[rank] = nb0 + incl - blocks;
       }
-      n += __popcll(bal);
-      nb += __shfl(incl, 63, 64);
+      cnt = __popcll(bal);
+      nblk = __shfl(incl, 63, 64);
+    };
+    if (nseg == 1 || nseg > kMaxSeg) {
+      if (w == 0) {
+        int n = 0, nb = 0;
+        for (int sg = 0; sg < nseg; ++sg) {
+          int cnt, nblk;
+          seg_items(sg, n, nb, true, cnt, nblk);
+          n += cnt;
+          nb += nblk;
+        }
+        if (lane == 0) {
+          bp[n] = nb;
+          s_info[4] = n;
+          s_info[5] = nb;
+        }
+      }
+    } else {
+      for (int sg = w; sg < nseg; sg += kFW) {
+        int cnt, nblk;
+        seg_items(sg, 0, 0, false, cnt, nblk);
+        if (lane == 0) { s_segn[sg] = cnt; s_segb[sg] = nblk; }
+      }
+      __syncthreads();
+      for (int sg = w; sg < nseg; sg += kFW) {
+        int n0 = 0, nb0 = 0;
+        for (int k = 0; k < sg; ++k) { n0 += s_segn[k]; nb0 += s_segb[k]; }
+        int cnt, nblk;
+        seg_items(sg, n0, nb0, true, cnt, nblk);
+        if (sg == nseg - 1 && lane == 0) {
+          bp[n0 + cnt] = nb0 + nblk;
+          s_info[4] = n0 + cnt;
+          s_info[5] = nb0 + nblk;
+        }
+      }
     }
-    if (lane == 0) {
-      bp[n] = nb;
-      s_info[4] = n;
-      s_info[5] = nb;
+  } else {
+    // items: the union's chunks in ascending order with their head masks, and
+    // the prefix count of 32-token blocks
+    if (w == 0) {
+      int n = 0, nb = 0;
+      for (int c0 = 0; c0 <= cur; c0 += 64) {
+        const int c = c0 + lane;
+        const int m = c <= cur ? umask[c] : 0;
+        const uint64_t bal = __ballot(m != 0);
+        const int rank = n + __popcll(bal & ((1ull << lane) - 1ull));
+        const int ntok = c < cur ? C : p + 1 - cur * C;
+        int blocks = m != 0 ? (ntok + 31) / 32 : 0;
+        // inclusive scan of the block counts over the wave
+        int incl = blocks;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+          const int y = __shfl_up(incl, off, 64);
+          if (lane >= off) incl += y;
+        }
+        if (m != 0) {
+          item_c[rank] = c;
+          item_m[rank] = m;
+          bp[rank] = nb + incl - blocks;
+        }
+        n += __popcll(bal);
+        nb += __shfl(incl, 63, 64);
+      }
+      if (lane == 0) {
+        bp[n] = nb;
+        s_info[4] = n;
+        s_info[5] = nb;
+      }
     }
   }
   __syncthreads();
@@ -774,18 +980,25 @@ bool wide_launch(const FusedArgs& a, int splits, int DP, size_t dyn) {
   return blocks >= (int64_t)kWideBlocksPerWorkgroup * per_row;
 }
 
-template <int DT, int DP>
+template <int DT, int DP, bool WROUTE>
 int launch_fused(const FusedArgs& a, int splits, size_t dyn, hipStream_t st) {
   const dim3 grid = a.sched != nullptr ? dim3((unsigned)a.n_sched)
                                         : dim3((unsigned)splits, (unsigned)(a.Nq * a.Hkv * a.Vg));
   bool wide = false;
   if constexpr (DP <= 128) {
     wide = wide_launch(a, splits, DP, dyn);
-    if (wide) hipLaunchKernelGGL((fused_kernel<DT, DP, kFwWide>), grid, dim3(64 * kFwWide), dyn, st, a);
+    if (wide) hipLaunchKernelGGL((fused_kernel<DT, DP, kFwWide, WROUTE>), grid, dim3(64 * kFwWide), dyn, st, a);
   }
-  if (!wide) hipLaunchKernelGGL((fused_kernel<DT, DP, kFwNarrow>), grid, dim3(64 * kFwNarrow), dyn, st, a);
+  if (!wide) hipLaunchKernelGGL((fused_kernel<DT, DP, kFwNarrow, WROUTE>), grid, dim3(64 * kFwNarrow), dyn, st, a);
   hipLaunchKernelGGL((merge_kernel<DT>), dim3((unsigned)(a.Nq * a.Hq)), dim3(64 * kMergeWaves), 0, st, a);
   return moba_launch_status("decode_fused");
+}
+
+template <int DT, int DP>
+int launch_fused(const FusedArgs& a, int splits, size_t dyn, hipStream_t st) {
+  // closed chunks of a row are at most `width`
+  return a.width > 64 && !a.dense ? launch_fused<DT, DP, true>(a, splits, dyn, st)
+                                  : launch_fused<DT, DP, false>(a, splits, dyn, st);
 }
 
 template <int DT>

@@ -92,37 +92,6 @@ __global__ __launch_bounds__(256) void chunk_means_kernel(const uint16_t* __rest
 // order, unchanged.
 constexpr int kRouteTile = 32;
 
-// acc = fma(lane (row base + j) of m, q[j], acc) for j = 0..15 in order: the
-// fma takes its first operand through a DPP row broadcast (row_newbcast),
-// which the compiler does not fold on its own.  The leading s_nop covers the
-// DPP read-after-VALU-write hazard on m (the compiler does not look inside
-// the block).
-MOBA_DEV float fma16_bcast(float acc, float m, const float* q) {
-  asm volatile(
-      "s_nop 1\n"
-      "v_fmac_f32_dpp %0, %1, %2 row_newbcast:0 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %3 row_newbcast:1 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %4 row_newbcast:2 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %5 row_newbcast:3 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %6 row_newbcast:4 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %7 row_newbcast:5 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %8 row_newbcast:6 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %9 row_newbcast:7 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %10 row_newbcast:8 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %11 row_newbcast:9 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %12 row_newbcast:10 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %13 row_newbcast:11 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %14 row_newbcast:12 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %15 row_newbcast:13 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %16 row_newbcast:14 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %17 row_newbcast:15 row_mask:0xf bank_mask:0xf\n"
-      : "+v"(acc)
-      : "v"(m), "v"(q[0]), "v"(q[1]), "v"(q[2]), "v"(q[3]), "v"(q[4]), "v"(q[5]), "v"(q[6]),
-        "v"(q[7]), "v"(q[8]), "v"(q[9]), "v"(q[10]), "v"(q[11]), "v"(q[12]), "v"(q[13]),
-        "v"(q[14]), "v"(q[15]));
-  return acc;
-}
-
 // DE: the head dim when it is DP exactly (no per-piece bound checks), else 0.
 template <int DT, int DP, int DE>
 __global__ __launch_bounds__(256) void route_kernel(const uint16_t* __restrict__ q, int T, int Hq,
@@ -213,14 +182,14 @@ __global__ __launch_bounds__(256) void route_kernel(const uint16_t* __restrict__
       float acc = 0.0f;
 #pragma unroll
       for (int i = 0; i < NM; ++i) {
-        if constexpr (QF32) {
-          acc = fma16_bcast(acc, mv[i], qf + 16 * i);
-        } else {
-          float qq[16];
+        float qa[8], qb[8];
 #pragma unroll
-          for (int e = 0; e < 16; ++e) qq[e] = to_f32<DT>(qv[2 * i + e / 8][e % 8]);
-          acc = fma16_bcast(acc, mv[i], qq);
+        for (int e = 0; e < 8; ++e) {
+          qa[e] = QF32 ? qf[16 * i + e] : to_f32<DT>(qv[2 * i][e]);
+          qb[e] = QF32 ? qf[16 * i + 8 + e] : to_f32<DT>(qv[2 * i + 1][e]);
         }
+        acc = fma8_bcast<0>(acc, mv[i], qa);
+        acc = fma8_bcast<8>(acc, mv[i], qb);
       }
       if (!(live && f >= f0 && f < f1)) continue;
       const int c = f + b;

@@ -389,3 +389,28 @@ def test_virtual_kv_heads_prepared(cuda_device, graph, hq, hk, dim, dtype):
     assert cache.lengths == (35, 38, 35)
     q = rand((3, hq, dim), dtype, 230)
     check(cache, cache.attend(q, sequence_ids=[0, 1, 2], topk=4), q)
+
+
+@pytest.mark.parametrize("tied", [False, True])
+@pytest.mark.parametrize("hq,hk,topk", [(8, 2, 4), (32, 1, 9)])
+def test_wide_route_top_k(cuda_device, tied, hq, hk, topk):
+    """More than 64 closed chunks per row: the route takes the wave-wide top-k
+    path.  Routes are compared bit for bit with the oracle's rank rule,
+    including exact ties (identical chunk means, ties to the lowest chunk)."""
+    Paged, _ = _caches()
+    dim, chunk, n = 64, 4, 600
+    cache = Paged(2, 640, hk, dim, page_size=7, chunk_size=chunk, dtype=torch.bfloat16)
+    k = rand((n, hk, dim), torch.bfloat16, 241)
+    if tied:  # chunks repeat every 8: many exactly equal means and scores
+        k = k.view(n // chunk, chunk, hk, dim)
+        k = k[torch.arange(n // chunk) % 8].reshape(n, hk, dim).contiguous()
+    v = rand((n, hk, dim), torch.bfloat16, 242)
+    cache.append(k, v, sequence_ids=[0], cu_seqlens=[0, n])
+    cache.append(k[:301], v[:301], sequence_ids=[1], cu_seqlens=[0, 301])
+    q = rand((2, hq, dim), torch.bfloat16, 243)
+    check(cache, cache.attend(q, sequence_ids=[0, 1], topk=topk), q)
+    with cache.prepare_decode([0, 1], hq, topk=topk) as p:
+        for step in range(3):
+            qs = rand((2, hq, dim), torch.bfloat16, 250 + step)
+            kn = rand((2, hk, dim), torch.bfloat16, 260 + step)
+            check(cache, p.step(qs, kn, kn), qs)
