@@ -81,8 +81,10 @@ class PrefillPlan:
         self.kv_tiles_list = self._kv_tile_order(att_chunk, fidx, cu, chunk_batch, cu_chunk)
         self.n_kv_tiles = len(self.kv_tiles_list) // 4
         # few kv heads leave too few key tiles to fill the chip: split each
-        # tile's query rows over several workgroups (fp32 partials + reduce)
-        self.kv_splits = (max(1, min(8, 1024 // max(1, self.n_kv_tiles)))
+        # tile's query rows over several workgroups (fp32 partials + reduce);
+        # about 1536 workgroups in all (cfg2: 6 splits, 1.50-1.52 ms per step
+        # against 1.53 with 4 and 8, 1.54-1.58 with 12-16)
+        self.kv_splits = (max(1, min(8, 1536 // max(1, self.n_kv_tiles)))
                           if head_dim % 8 == 0 else 1)
         kv_flat = self.kv_tiles_list
 
