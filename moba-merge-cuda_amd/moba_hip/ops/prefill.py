@@ -73,6 +73,12 @@ class PrefillPlan:
         for c in filtered:
             ns = cu[chunk_batch[c] + 1] - cu_chunk[c + 1]
             max_tiles += hkv * ((self.groups * ns + BLOCK_ROWS - 1) // BLOCK_ROWS)
+        # every (token, q head) row sits in at most `remote` experts, and an
+        # expert's last tile may be partial: at most rows / BLOCK_ROWS + E
+        # tiles.  (The remote kernels' grids are this bound; workgroups past
+        # the actual count, known only on the device, return at once.)
+        rows_bound = cu[-1] * hq * self.remote
+        max_tiles = min(max_tiles, -(-rows_bound // BLOCK_ROWS) + self.num_experts)
         self.max_remote_tiles = max_tiles
         self.chunk_start = [cu_chunk[c] for c in filtered]
         # key-major backward tiles: (chunk, first key, filtered index or -1)
