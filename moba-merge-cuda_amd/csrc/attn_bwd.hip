@@ -36,7 +36,7 @@ __global__ __launch_bounds__(256) void delta_kernel(const uint16_t* __restrict__
                                                     const uint16_t* __restrict__ g,
                                                     const float* __restrict__ lse, int64_t rows,
                                                     int D, float* __restrict__ delta,
-                                                    float* __restrict__ lse2) {
+                                                    float scale, float* __restrict__ lse_k) {
   const int sub = threadIdx.x & 15;
   const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
   float acc = 0.0f;
@@ -51,7 +51,7 @@ __global__ __launch_bounds__(256) void delta_kernel(const uint16_t* __restrict__
   for (int off = 8; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 16);
   if (row < rows && sub == 0) {
     delta[row] = acc;
-    lse2[row] = lse[row] * kLog2e;
+    lse_k[row] = lse[row] / scale;
   }
 }
 
@@ -128,7 +128,7 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a
     }
   }
   u16x8_t qf[QB][NKS], gf[QB][NKS];
-  float lse2[QB], dl[QB];
+  float lse2[QB], lk[QB], dl[QB];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     const int64_t row = (int64_t)s[qb] * a.Hq + h[qb];
@@ -139,13 +139,15 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a
       qf[qb][ks] = ok ? ld8(a.q + row * D + d) : zero8();
       gf[qb][ks] = ok ? ld8(a.dout + row * D + d) : zero8();
     }
-    lse2[qb] = valid[qb] ? a.lse[row] * kLog2e : INFINITY;
+    const float lr = valid[qb] ? a.lse[row] : INFINITY;
+    lse2[qb] = lr * kLog2e;
+    lk[qb] = lr / a.scale;
     dl[qb] = valid[qb] ? a.delta[row] : 0.0f;
   }
   if constexpr (REMOTE && DP <= 128) {
     // The key-major dK/dV kernel reads the expert rows packed contiguously in
     // row_off order; this kernel holds exactly those rows, so it writes the
-    // packed q / dO / lse2 / delta (the values delta_kernel and the loads above
+    // packed q / dO / lse_k / delta (the values delta_kernel and the loads above
     // produce) instead of a separate gather pass.
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
@@ -160,7 +162,7 @@ __global__ __launch_bounds__(256, attn_occupancy<DP>()) void dq_kernel(BwdArgs a
         }
       }
       if (hh == 0) {
-        a.pack_lse2[m] = lse2[qb];
+        a.pack_lse_k[m] = lk[qb];
         a.pack_delta[m] = dl[qb];
       }
     }
@@ -924,7 +926,7 @@ int launch_bwd(const BwdArgs& a, int n_self, int n_kv, int max_remote, int parts
   const int64_t rows = (int64_t)a.T * a.Hq;
   if (parts & 1) {
     hipLaunchKernelGGL(delta_kernel<DT>, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, st,
-                       a.out, a.dout, a.lse, rows, a.D, a.delta, a.lse2);
+                       a.out, a.dout, a.lse, rows, a.D, a.delta, a.scale, a.lse_k);
     if (max_remote > 0 && a.R > 0)
       hipLaunchKernelGGL((dq_kernel<DT, DP, true, attn_qb<DP>()>), dim3((max_remote + 7) / 8 * 8), dim3(256), 0, st, a);
     if (n_self > 0)
@@ -1009,12 +1011,12 @@ extern "C" int moba_hip_prefill_bwd(const void* q, const void* k, const void* v,
     a.part_dkv = (float*)(ws + dkdv_sched_bytes(n_kv_tiles, kv_splits));
   }
   a.dq = (uint16_t*)dq; a.dk = (uint16_t*)dk; a.dv = (uint16_t*)dv;
-  a.lse2 = delta + (int64_t)T * Hq;
+  a.lse_k = delta + (int64_t)T * Hq;
   a.pack_rows = (R > 0 && D <= 128) ? (int64_t)T * Hq * R : 0;
   a.pack_q = (uint16_t*)pack;
   a.pack_g = a.pack_q + a.pack_rows * D;
-  a.pack_lse2 = (float*)(a.pack_g + a.pack_rows * D);
-  a.pack_delta = a.pack_lse2 + a.pack_rows;
+  a.pack_lse_k = (float*)(a.pack_g + a.pack_rows * D);
+  a.pack_delta = a.pack_lse_k + a.pack_rows;
   if (a.pack_rows > 0 && pack == nullptr) { moba_set_error("prefill_bwd: the pack workspace is required when R > 0 and head_dim <= 128"); return MOBA_ERR_ARG; }
   if (a.pack_rows * D * 2 >= ((int64_t)1 << 32)) { moba_set_error("prefill_bwd: packed expert rows must be smaller than 4 GiB (32-bit buffer offsets)"); return MOBA_ERR_ARG; }
   hipStream_t st = (hipStream_t)stream;

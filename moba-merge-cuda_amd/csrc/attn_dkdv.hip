@@ -13,9 +13,11 @@
 // owns keys 32w..32w+31 and holds their K and V rows as MFMA B operands and
 // their dK, dV accumulators.  For each 64-row tile of (Q, dO) rows it runs all
 // four products itself:
-//   S  = Q K^T,  dP = dO V^T         (A = Q / dO rows from LDS)
-//   P  = exp2(S*c - lse2), dS = P (dP - delta)
-//   dV += P^T dO,  dK += dS^T Q      (B = dO / Q through transposed LDS reads)
+//   X = lse_k - Q K^T,  Y = delta - dO V^T   (A = Q / dO rows from LDS, B = -K / -V)
+//   P  = exp2(-c X),  -dS = P Y
+//   dV += P^T dO,  -dK += (-dS)^T Q  (B = dO / Q through transposed LDS reads)
+// lse_k = lse / scale and delta start the accumulators, so the row terms cost
+// no element-wise work.
 // The D layout of S / dP (one key per lane) is the A layout of P^T / dS^T, so
 // P and dS never leave registers and the waves never wait for each other
 // inside a tile: one barrier per tile, where the LDS stages rotate.  Used for
@@ -45,7 +47,7 @@ __global__ __launch_bounds__(256, 1) void dkdv1_kernel(BwdArgs a) {
   constexpr int NDMA = kRows * NB / 256;        // blocks per thread per operand
   constexpr int NS = kStages;
   static_assert(NDMA >= 1, "tile smaller than one block per thread");
-  // Q / dO tiles (swz<DP> layout) and their rows' lse2 / delta in NS named
+  // Q / dO tiles (swz<DP> layout) and their rows' lse_k / delta in NS named
   // stages, filled by buffer loads straight into LDS NS - 1 tiles ahead.
   __shared__ __attribute__((aligned(16))) uint16_t Q0[kRows * DP];
   __shared__ __attribute__((aligned(16))) uint16_t G0[kRows * DP];
@@ -95,7 +97,7 @@ __global__ __launch_bounds__(256, 1) void dkdv1_kernel(BwdArgs a) {
   const int it_lo = s_lo, it_hi = min(s_hi, n_tiles);  // this workgroup's share
 
   // Every tile's rows are affine in the row number, so the loads need no row
-  // indices: self tiles read q / dO / lse2 / delta in place (row stride Hq),
+  // indices: self tiles read q / dO / lse_k / delta in place (row stride Hq),
   // expert tiles the packed copies (row stride 1).  Rows past the tile's
   // valid range read past num_records, i.e. zeros: a zero Q and dO row adds
   // nothing to dK or dV whatever its probability.  Thread t loads blocks
@@ -111,7 +113,7 @@ __global__ __launch_bounds__(256, 1) void dkdv1_kernel(BwdArgs a) {
     jrow[n] = q;
     jcol[n] = swz<DP>(q, (j % NB) * 8) - q * DP;
   }
-  // Per wave and tile: 2 * NDMA tile loads plus lse2 and delta of 16 rows,
+  // Per wave and tile: 2 * NDMA tile loads plus lse_k and delta of 16 rows,
   // always issued (tiles past it_hi load zeros into a stage nobody reads), so
   // the wait below is a constant.
   constexpr int kLoadsPerTile = 2 * NDMA + 2;
@@ -138,26 +140,28 @@ __global__ __launch_bounds__(256, 1) void dkdv1_kernel(BwdArgs a) {
       dma_lds16(make_rsrc(srcq, nb), Qd + jb * 8, off, 0);
       dma_lds16(make_rsrc(srcg, nb), Gd + jb * 8, off, 0);
     }
-    if (lane < 16) {  // wave w: lse2 and delta of rows 16w .. 16w + 15
+    if (lane < 16) {  // wave w: lse_k and delta of rows 16w .. 16w + 15
       const int q = wave_s * 16 + lane;
       const uint32_t lb = is_self ? lbytes : plbytes;
       const uint32_t off = q < nvalid ? (uint32_t)(r0 + q * rstride) * 4 : lb;
-      dma_lds4(make_rsrc(is_self ? a.lse2 : a.pack_lse2, lb), Ld + wave_s * 16, off, 0);
+      dma_lds4(make_rsrc(is_self ? a.lse_k : a.pack_lse_k, lb), Ld + wave_s * 16, off, 0);
       dma_lds4(make_rsrc(is_self ? a.delta : a.pack_delta, lb), Ld + kRows + wave_s * 16, off, 0);
     }
   };
   const uint32_t kq0 = swz_b128_base<DP>(lane);
   const uint32_t trb0 = swz_tr_base<DP>(lane, 0), trb1 = swz_tr_base<DP>(lane, 1);
-  const float c2 = a.scale_log2;
+  const float nc2 = -a.scale_log2;
 
-  u16x8_t kf[NKS], vf[NKS];                   // B operands: column = key, k = d
+  // B operands (column = key, k = d), negated: with the accumulators started
+  // at the row's lse_k and delta, the MFMAs produce lse_k - S and delta - dP
+  u16x8_t kf[NKS], vf[NKS];
 #pragma unroll
   for (int ks = 0; ks < NKS; ++ks) {
     const int d = ks * 16 + hh * 8;
     const bool ok = mykey < c_hi && d < D;
     const int64_t off = ((int64_t)mykey * a.Hkv + kh) * D + d;
-    kf[ks] = ok ? ld8(a.k + off) : zero8();
-    vf[ks] = ok ? ld8(a.v + off) : zero8();
+    kf[ks] = neg8(ok ? ld8(a.k + off) : zero8());
+    vf[ks] = neg8(ok ? ld8(a.v + off) : zero8());
   }
   // K / V rows must have landed before the tile loads start: the compiler's
   // own waits for them would otherwise also drain the tile loads in flight
@@ -172,19 +176,8 @@ __global__ __launch_bounds__(256, 1) void dkdv1_kernel(BwdArgs a) {
     const uint32_t kq = opaque(kq0), t0 = opaque(trb0), t1 = opaque(trb1);
     const bool is_self = it < G * n_self;
     const int sq0 = is_self ? self_begin + (it % n_self) * kRows : 0;
+    // D layout: lane holds rows 8j + 4hh + i of block qb
     f32x16_t sp[QB], dp[QB];
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) { sp[qb] = zero16(); dp[qb] = zero16(); }
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) {
-        const uint32_t o = qb * 32 * DP * 2 + swz_b128<DP>(kq, ks);
-        sp[qb] = mfma32<DT>(lds8(Qb, o), kf[ks], sp[qb]);
-        dp[qb] = mfma32<DT>(lds8(Gb, o), vf[ks], dp[qb]);
-      }
-    // P and dS as A operands (D layout: rows 8j + 4hh + i of block qb)
-    u16x8_t pa[QB][2], da[QB][2];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
@@ -193,11 +186,29 @@ __global__ __launch_bounds__(256, 1) void dkdv1_kernel(BwdArgs a) {
         const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(Lb + r0);
         const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(Lb + kRows + r0);
 #pragma unroll
+        for (int i = 0; i < 4; ++i) { sp[qb][4 * j + i] = l4[i]; dp[qb][4 * j + i] = d4[i]; }
+      }
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        const uint32_t o = qb * 32 * DP * 2 + swz_b128<DP>(kq, ks);
+        sp[qb] = mfma32<DT>(lds8(Qb, o), kf[ks], sp[qb]);
+        dp[qb] = mfma32<DT>(lds8(Gb, o), vf[ks], dp[qb]);
+      }
+    // P and -dS as A operands: P = exp2(c2 (S - lse_k)), -dS = P (delta - dP)
+    u16x8_t pa[QB][2], da[QB][2];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r0 = qb * 32 + 8 * j + 4 * hh;
+#pragma unroll
         for (int i = 0; i < 4; ++i) {
-          float p = fast_exp2(fmaf(sp[qb][4 * j + i], c2, -l4[i]));
+          float p = fast_exp2(sp[qb][4 * j + i] * nc2);
           if constexpr (MASK) p = (mykey < c_hi && (!is_self || mykey <= sq0 + r0 + i)) ? p : 0.0f;
           pa[qb][j >> 1][(j & 1) * 4 + i] = from_f32<DT>(p);
-          da[qb][j >> 1][(j & 1) * 4 + i] = from_f32<DT>(p * (dp[qb][4 * j + i] - d4[i]));
+          da[qb][j >> 1][(j & 1) * 4 + i] = from_f32<DT>(p * dp[qb][4 * j + i]);
         }
       }
 #pragma unroll
@@ -258,10 +269,10 @@ __global__ __launch_bounds__(256, 1) void dkdv1_kernel(BwdArgs a) {
       if (key >= c_hi) continue;
       const int64_t o = ((int64_t)key * a.Hkv + kh) * D + d;
       if (slot >= 0) {
-        pk[(key - key0) * D + d] = dk[i][r];
+        pk[(key - key0) * D + d] = -dk[i][r];
         pv[(key - key0) * D + d] = dv[i][r];
       } else {
-        a.dk[o] = from_f32<DT>(dk[i][r] * a.scale);
+        a.dk[o] = from_f32<DT>(dk[i][r] * -a.scale);
         a.dv[o] = from_f32<DT>(dv[i][r]);
       }
     }

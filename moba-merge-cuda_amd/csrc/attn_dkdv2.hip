@@ -13,12 +13,16 @@
 // A workgroup of 8 waves owns 128 keys of one chunk and one KV head as 4 wave
 // pairs of 32 keys; the two waves of a pair share a SIMD.  For 64-row tiles
 // of (Q, dO) rows, at step t:
-//   role P (K in registers, dV accumulators):
-//       one MFMA block: S_t = Q_t K^T  interleaved with  dV += P_{t-1}^T dO_{t-1}
-//       then P_t = exp2(S_t*c - lse2) -> registers and LDS (input dtype)
-//   role D (V in registers, dK accumulators):
-//       dS_{t-1} = P_{t-1} (dP_{t-1} - delta)          (P from LDS)
-//       then one MFMA block: dK += dS_{t-1}^T Q_{t-1}  interleaved with  dP_t = dO_t V^T
+//   role P (-K in registers, dV accumulators):
+//       one MFMA block: X_t = lse_k - Q_t K^T  interleaved with  dV += P_{t-1}^T dO_{t-1}
+//       then P_t = exp2(-c X_t) -> registers and LDS (input dtype)
+//   role D (-V in registers, -dK accumulators):
+//       -dS_{t-1} = P_{t-1} Y_{t-1}                    (P from LDS)
+//       then one MFMA block: -dK += (-dS_{t-1})^T Q_{t-1}  interleaved with
+//       Y_t = delta - dO_t V^T
+// The row terms enter as the accumulators' start values (lse_k = lse / scale
+// and delta of the tile's rows, read from LDS when the block starts), so the
+// element-wise phases read no per-row values.
 // Each role alternates a VALU phase and an MFMA block of two independent
 // accumulator chains, in opposite order, so the SIMD's MFMA unit is fed by
 // one wave while the other does its element-wise work.  Role D runs one tile
@@ -45,7 +49,7 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
   constexpr int NB = DP / 8;                    // 16-byte blocks per row
   constexpr int NDMA = kRows * NB / 512;        // blocks per thread per operand
   static_assert(NDMA >= 1 && kRows * NB % 512 == 0, "one block per thread at least");
-  // Q / dO tiles (swz<DP> layout) and their rows' lse2 / delta, three named
+  // Q / dO tiles (swz<DP> layout) and their rows' lse_k / delta, three named
   // stages; P of the last two tiles per pair: [tile & 1][pair][qb][half][lane].
   __shared__ __attribute__((aligned(16))) uint16_t Q0[kRows * DP];
   __shared__ __attribute__((aligned(16))) uint16_t G0[kRows * DP];
@@ -95,10 +99,10 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
   const int n_tiles = G * n_self + (n_rem + kRows - 1) / kRows;
   const int it_lo = s_lo, it_hi = min(s_hi, n_tiles);  // this workgroup's share
 
-  // Tile loads: self tiles read q / dO / lse2 / delta in place (row stride
+  // Tile loads: self tiles read q / dO / lse_k / delta in place (row stride
   // Hq), expert tiles the packed copies (row stride 1); rows past the tile's
   // valid range read past num_records, i.e. zeros, and a zero Q and dO row
-  // adds nothing.  Thread t loads blocks n * 512 + t; wave w loads lse2 and
+  // adds nothing.  Thread t loads blocks n * 512 + t; wave w loads lse_k and
   // delta of rows 8w .. 8w + 7.
   const uint32_t qbytes = (uint32_t)((int64_t)a.T * a.Hq * D * 2);
   const uint32_t pbytes = (uint32_t)((int64_t)a.pack_rows * D * 2);
@@ -148,14 +152,14 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
       const int q = wave_s * 8 + lane;
       const uint32_t lb = is_self ? lbytes : plbytes;
       const uint32_t off = q < nvalid ? (uint32_t)(r0 + q * rstride) * 4 : lb;
-      dma_lds4(make_rsrc(is_self ? a.lse2 : a.pack_lse2, lb), Ld + wave_s * 8, off, 0);
+      dma_lds4(make_rsrc(is_self ? a.lse_k : a.pack_lse_k, lb), Ld + wave_s * 8, off, 0);
       dma_lds4(make_rsrc(is_self ? a.delta : a.pack_delta, lb), Ld + kRows + wave_s * 8, off, 0);
     }
   };
 
   const uint32_t kq0 = swz_b128_base<DP>(lane);
   const uint32_t trb0 = swz_tr_base<DP>(lane, 0), trb1 = swz_tr_base<DP>(lane, 1);
-  const float c2 = a.scale_log2;
+  const float nc2 = -a.scale_log2;
 
   // causal rows that end before the pair's first key contribute nothing
   auto skipped = [&](Cur t) __attribute__((always_inline)) {
@@ -163,10 +167,10 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
   };
   // One MFMA block of up to two independent chains, interleaved step by
   // step, each with its operand reads PF steps ahead (PF = 3 when both run):
-  //   chain A: sp (rows x keys) = A (rows, b128 reads) x kv (keys in registers)
+  //   chain A: sp (rows x keys) = Li (row terms) + A (rows, b128 reads) x kv (keys in registers)
   //   chain B: acc (keys x d) += op^T (in registers) x B (rows, transposed reads)
   // Both chains are NKS * QB = NDB * QB * 2 MFMAs long.
-  auto block = [&](auto da_tag, auto db_tag, const uint16_t* A, const u16x8_t (&kv)[NKS],
+  auto block = [&](auto da_tag, auto db_tag, const float* Li, const uint16_t* A, const u16x8_t (&kv)[NKS],
                    f32x16_t (&sp)[QB], const uint16_t* B, const u16x8_t (&op)[QB][2],
                    f32x16_t (&acc)[NDB]) __attribute__((always_inline)) {
     constexpr bool DA = decltype(da_tag)::value, DB = decltype(db_tag)::value;
@@ -185,9 +189,15 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
       return lds_tr8(B, ro + swz_tr<DP>(t0, i % NDB), ro + swz_tr<DP>(t1, i % NDB));
     };
     u16x8_t ra[PF], rb[PF];
-    if constexpr (DA) {
+    if constexpr (DA) {  // D layout: lane holds rows 8j + 4hh + i of block qb
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) sp[qb] = zero16();
+      for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(Li + qb * 32 + 8 * j + 4 * hh);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sp[qb][4 * j + i] = l4[i];
+        }
     }
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
@@ -211,16 +221,16 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
     }
   };
   // the block for runtime flags (chain A: current tile, chain B: previous tile)
-  auto run_block = [&](bool cur, bool prev, const uint16_t* A, const u16x8_t (&kv)[NKS],
+  auto run_block = [&](bool cur, bool prev, const float* Li, const uint16_t* A, const u16x8_t (&kv)[NKS],
                        f32x16_t (&sp)[QB], const uint16_t* B, const u16x8_t (&op)[QB][2],
                        f32x16_t (&acc)[NDB]) __attribute__((always_inline)) {
     // the wave in its MFMA block issues ahead of its partner's element-wise
     // phase on the shared SIMD
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_setprio(1);
-    if (cur && prev) block(std::true_type{}, std::true_type{}, A, kv, sp, B, op, acc);
-    else if (cur) block(std::true_type{}, std::false_type{}, A, kv, sp, B, op, acc);
-    else if (prev) block(std::false_type{}, std::true_type{}, A, kv, sp, B, op, acc);
+    if (cur && prev) block(std::true_type{}, std::true_type{}, Li, A, kv, sp, B, op, acc);
+    else if (cur) block(std::true_type{}, std::false_type{}, Li, A, kv, sp, B, op, acc);
+    else if (prev) block(std::false_type{}, std::true_type{}, Li, A, kv, sp, B, op, acc);
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_setprio(0);
     __builtin_amdgcn_sched_barrier(0);
@@ -228,34 +238,34 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
 
   auto body = [&](auto role_tag) __attribute__((always_inline)) {
     constexpr bool ROLE_P = decltype(role_tag)::value;
-    // K (role P) or V (role D) rows: B operands, column = key, k = d
+    // -K (role P) or -V (role D) rows: B operands, column = key, k = d
     u16x8_t kv[NKS];
     const uint16_t* kvsrc = ROLE_P ? a.k : a.v;
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
       const int d = ks * 16 + hh * 8;
-      kv[ks] = (mykey < c_hi && d < D) ? ld8(kvsrc + ((int64_t)mykey * a.Hkv + kh) * D + d) : zero8();
+      kv[ks] = neg8((mykey < c_hi && d < D) ? ld8(kvsrc + ((int64_t)mykey * a.Hkv + kh) * D + d) : zero8());
     }
     // the rows must have landed before the tile loads start: the compiler's
     // own waits for them would otherwise also drain the tile loads in flight
     __builtin_amdgcn_s_waitcnt(0x0F70);
-    f32x16_t acc[NDB];                          // dV (role P) or dK (role D)
+    f32x16_t acc[NDB];                          // dV (role P) or -dK (role D)
 #pragma unroll
     for (int i = 0; i < NDB; ++i) acc[i] = zero16();
-    // role P: S of the current tile; role D: dP of the last computed tile
+    // role P: lse_k - S of the current tile; role D: delta - dP of the last computed tile
     f32x16_t sp[QB];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) sp[qb] = zero16();
-    // role P: P of the previous tile; role D: dS of the previous tile
+    // role P: P of the previous tile; role D: -dS of the previous tile
     u16x8_t op[QB][2];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) op[qb][0] = op[qb][1] = zero8();
 
     // role P, tile t in stage (Qc, Lc), previous tile's dO in Gp:
-    //   S_t and dV += P_prev^T dO_prev in one block, then P_t -> op and LDS
+    //   X_t and dV += P_prev^T dO_prev in one block, then P_t -> op and LDS
     auto p_step = [&](const uint16_t* Qc, const float* Lc, const uint16_t* Gp, Cur t, bool cur,
                       bool prev) __attribute__((always_inline)) {
-      run_block(cur, prev, Qc, kv, sp, Gp, op, acc);
+      run_block(cur, prev, Lc, Qc, kv, sp, Gp, op, acc);
       if (!cur) return;
       const bool is_self = t.g < G;
       const int sq0 = is_self ? self_begin + t.s * kRows : 0;
@@ -267,10 +277,9 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int r0 = qb * 32 + 8 * j + 4 * hh;
-            const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(Lc + r0);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              float p = fast_exp2(fmaf(sp[qb][4 * j + i], c2, -l4[i]));
+              float p = fast_exp2(sp[qb][4 * j + i] * nc2);
               if constexpr (MASK) p = (mykey < c_hi && (!is_self || mykey <= sq0 + r0 + i)) ? p : 0.0f;
               op[qb][j >> 1][(j & 1) * 4 + i] = from_f32<DT>(p);
             }
@@ -283,9 +292,9 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
         Px[t.it & 1][pair][qb][1][lane] = op[qb][1];
       }
     };
-    // role D: dS_prev = P_prev (dP_prev - delta) from LDS and registers, then
-    // dK += dS_prev^T Q_prev and dP_t = dO_t V^T in one block
-    auto d_step = [&](const uint16_t* Gc, const uint16_t* Qp, const float* Lp, Cur t, bool cur,
+    // role D: -dS_prev = P_prev Y_prev (P from LDS), then
+    // -dK += (-dS_prev)^T Q_prev and Y_t = delta - dO_t V^T in one block
+    auto d_step = [&](const uint16_t* Gc, const float* Lc, const uint16_t* Qp, Cur t, bool cur,
                       bool prev) __attribute__((always_inline)) {
       if (prev) {
         const int b = (t.it - 1) & 1;
@@ -293,17 +302,15 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
         for (int qb = 0; qb < QB; ++qb) {
           const u16x8_t px[2] = {Px[b][pair][qb][0][lane], Px[b][pair][qb][1][lane]};
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(Lp + kRows + qb * 32 + 8 * j + 4 * hh);
+          for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               const int r = 4 * j + i, h2 = j >> 1, x = (j & 1) * 4 + i;
-              op[qb][h2][x] = from_f32<DT>(to_f32<DT>(px[h2][x]) * (sp[qb][r] - d4[i]));
+              op[qb][h2][x] = from_f32<DT>(to_f32<DT>(px[h2][x]) * sp[qb][r]);
             }
-          }
         }
       }
-      run_block(cur, prev, Gc, kv, sp, Qp, op, acc);
+      run_block(cur, prev, Lc + kRows, Gc, kv, sp, Qp, op, acc);
     };
     // one tile: stage c holds tile tc, stage p the tile before (computed when
     // pv), stage n receives the next tile; afterwards this wave's loads of
@@ -318,7 +325,7 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
       __builtin_amdgcn_sched_barrier(0);  // the next tile's loads go out first
       const bool cur = tc.it < it_hi && !skipped(tc);
       if constexpr (ROLE_P) p_step(Qc, Lc, Gp, tc, cur, pv);
-      else d_step(Gc, Qp, Lp, tc, cur, pv);
+      else d_step(Gc, Lc, Qp, tc, cur, pv);
       pv = cur;
       tc = tn;
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
@@ -342,7 +349,7 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
     float* pdst = a.part_dkv + (int64_t)max(slot, 0) * kv_slot_floats(D) +
                   (ROLE_P ? kKvTileKeys * D : 0);
     uint16_t* dst = ROLE_P ? a.dv : a.dk;
-    const float osc = ROLE_P ? 1.0f : a.scale;
+    const float psc = ROLE_P ? 1.0f : -1.0f, osc = ROLE_P ? 1.0f : -a.scale;
 #pragma unroll
     for (int i = 0; i < NDB; ++i) {
       const int d = i * 32 + qi;
@@ -352,7 +359,7 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
         const int key = pkey0 + 8 * (r >> 2) + 4 * hh + (r & 3);
         if (key >= c_hi) continue;
         const int64_t o = ((int64_t)key * a.Hkv + kh) * D + d;
-        if (slot >= 0) pdst[(key - key0) * D + d] = acc[i][r];
+        if (slot >= 0) pdst[(key - key0) * D + d] = acc[i][r] * psc;
         else dst[o] = from_f32<DT>(acc[i][r] * osc);
       }
     }

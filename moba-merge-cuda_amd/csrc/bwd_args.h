@@ -28,7 +28,7 @@ struct BwdArgs {
   const int* counts;
   const int* rows;
   float* delta;      // [T*Hq] rowsum(dO * O)
-  float* lse2;       // [T*Hq] lse * log2(e)
+  float* lse_k;      // [T*Hq] lse / scale: the row's log-sum-exp in q.k units
   uint16_t* part_dq;  // remote dQ slots, input dtype
   // Row-split schedule (kv_splits > 1, built on the device by
   // dkdv_sched_kernel): kv_sched[4 * workgroup] = (kv tile, first row tile,
@@ -43,11 +43,11 @@ struct BwdArgs {
   uint16_t* dk;
   uint16_t* dv;
   // Expert rows packed contiguously in row_off order for the key-major
-  // kernel: pack_rows (= T*Hq*R) rows of q, dO, lse2 and delta, written by
+  // kernel: pack_rows (= T*Hq*R) rows of q, dO, lse_k and delta, written by
   // the remote dq kernel.
   uint16_t* pack_q;
   uint16_t* pack_g;
-  float* pack_lse2;
+  float* pack_lse_k;
   float* pack_delta;
   int64_t pack_rows;
 };

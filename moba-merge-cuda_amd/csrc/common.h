@@ -89,6 +89,13 @@ MOBA_DEV u16x8_t zero8() {
   return z;
 }
 
+// sign flip of 8 bf16 / fp16 values (exact)
+MOBA_DEV u16x8_t neg8(u16x8_t x) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] ^= 0x8000;
+  return x;
+}
+
 MOBA_DEV u16x8_t ld8(const uint16_t* p) { return *reinterpret_cast<const u16x8_t*>(p); }
 MOBA_DEV void st8(uint16_t* p, const u16x8_t& v) { *reinterpret_cast<u16x8_t*>(p) = v; }
 
