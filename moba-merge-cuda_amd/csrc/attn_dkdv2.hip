@@ -31,7 +31,8 @@
 // stages hold tiles t - 1, t and t + 1 (loading).  The expert rows come
 // packed contiguously (written by the remote dq kernel), so every tile is affine in the row
 // number and is loaded HBM -> LDS by buffer loads issued from inline
-// assembly (the waits are placed here).
+// assembly (the waits are placed here): role D waves issue their share when
+// the step starts, role P waves between the MFMAs of their block.
 #include <type_traits>
 
 #include "common.h"
@@ -42,6 +43,10 @@ namespace {
 
 constexpr int kPairKeys = 32;   // keys per wave pair
 constexpr int kRows = 64;       // query rows per tile
+// role P issues load piece k of the next tile after MFMA step kDmaAt + 2k
+// of its block (the loads then overlap the block instead of stalling the
+// start of the step)
+constexpr int kDmaAt = 6;
 
 template <int DT, int DP>
 __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
@@ -126,7 +131,16 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
     if (t.g < G && t.s == n_self) { t.s = 0; ++t.g; }
     return t;
   };
-  auto dma = [&](uint16_t* Qd, uint16_t* Gd, float* Ld, Cur t) __attribute__((always_inline)) {
+  // A tile's loads as kPieces pieces: k < 2 NDMA loads Q (k even) or dO
+  // block k / 2 of this thread, k = 2 NDMA the rows' lse_k and delta.
+  struct Plan {
+    const uint16_t* sq; const uint16_t* sg; const float* sl;
+    uint32_t nb, lb, loff;
+    uint32_t off[NDMA];
+  };
+  constexpr int kPieces = 2 * NDMA + 1;
+  static_assert(kDmaAt + 2 * (kPieces - 1) < NKS * QB, "every piece is issued inside the block");
+  auto plan = [&](Cur t) __attribute__((always_inline)) {
     const bool is_self = t.g < G;
     int r0 = 0, rstride = 1, nvalid = 0;
     if (t.it >= it_hi) {
@@ -136,25 +150,38 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
     } else {
       r0 = rbase + t.s * kRows; rstride = 1; nvalid = min(kRows, n_rem - t.s * kRows);
     }
-    const uint16_t* srcq = is_self ? a.q : a.pack_q;
-    const uint16_t* srcg = is_self ? a.dout : a.pack_g;
-    const uint32_t nb = is_self ? qbytes : pbytes;
+    Plan pl;
+    pl.sq = is_self ? a.q : a.pack_q;
+    pl.sg = is_self ? a.dout : a.pack_g;
+    // delta and lse_k are adjacent arrays (delta first in place, lse_k first
+    // in the pack): one load of 16 lanes brings both
+    pl.sl = is_self ? a.delta : a.pack_lse_k;
+    pl.nb = is_self ? qbytes : pbytes;
+    pl.lb = 2 * (is_self ? lbytes : plbytes);
 #pragma unroll
     for (int n = 0; n < NDMA; ++n) {
       const int q = jrow[n], col = jcol[n];
-      const uint32_t off = (q < nvalid && col < D)
-                               ? (uint32_t)(((int64_t)(r0 + q * rstride) * D + col) * 2) : nb;
-      const int jb = n * 512 + wave_s * 64;   // first block of this wave's 64
-      dma_lds16(make_rsrc(srcq, nb), Qd + jb * 8, off, 0);
-      dma_lds16(make_rsrc(srcg, nb), Gd + jb * 8, off, 0);
+      pl.off[n] = (q < nvalid && col < D) ? (uint32_t)(((int64_t)(r0 + q * rstride) * D + col) * 2) : pl.nb;
     }
-    if (lane < 8) {
-      const int q = wave_s * 8 + lane;
-      const uint32_t lb = is_self ? lbytes : plbytes;
-      const uint32_t off = q < nvalid ? (uint32_t)(r0 + q * rstride) * 4 : lb;
-      dma_lds4(make_rsrc(is_self ? a.lse_k : a.pack_lse_k, lb), Ld + wave_s * 8, off, 0);
-      dma_lds4(make_rsrc(is_self ? a.delta : a.pack_delta, lb), Ld + kRows + wave_s * 8, off, 0);
+    // lanes 0..7: lse_k of rows 8w .. 8w + 7, lanes 8..15: their delta
+    const int ql = wave_s * 8 + (lane & 7);
+    const uint32_t l_at = (lane < 8) == is_self ? pl.lb / 2 : 0;  // lse_k half
+    pl.loff = ql < nvalid ? l_at + (uint32_t)(r0 + ql * rstride) * 4 : pl.lb;
+    return pl;
+  };
+  auto piece = [&](const Plan& pl, int k, uint16_t* Qd, uint16_t* Gd, float* Ld) __attribute__((always_inline)) {
+    if (k < 2 * NDMA) {
+      const int jb = (k >> 1) * 512 + wave_s * 64;   // first block of this wave's 64
+      if (k & 1) dma_lds16(make_rsrc(pl.sg, pl.nb), Gd + jb * 8, pl.off[k >> 1], 0);
+      else dma_lds16(make_rsrc(pl.sq, pl.nb), Qd + jb * 8, pl.off[k >> 1], 0);
+    } else if (lane < 16) {
+      dma_lds4(make_rsrc(pl.sl, pl.lb), Ld + wave_s * 16, pl.loff, 0);
     }
+  };
+  auto dma = [&](uint16_t* Qd, uint16_t* Gd, float* Ld, Cur t) __attribute__((always_inline)) {
+    const Plan pl = plan(t);
+#pragma unroll
+    for (int k = 0; k < kPieces; ++k) piece(pl, k, Qd, Gd, Ld);
   };
 
   const uint32_t kq0 = swz_b128_base<DP>(lane);
@@ -172,7 +199,7 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
   // Both chains are NKS * QB = NDB * QB * 2 MFMAs long.
   auto block = [&](auto da_tag, auto db_tag, const float* Li, const uint16_t* A, const u16x8_t (&kv)[NKS],
                    f32x16_t (&sp)[QB], const uint16_t* B, const u16x8_t (&op)[QB][2],
-                   f32x16_t (&acc)[NDB]) __attribute__((always_inline)) {
+                   f32x16_t (&acc)[NDB], auto&& side) __attribute__((always_inline)) {
     constexpr bool DA = decltype(da_tag)::value, DB = decltype(db_tag)::value;
     constexpr int N = NKS * QB, PF = (DA && DB) ? 3 : 6;
     static_assert(N == NDB * QB * 2, "chain lengths");
@@ -194,7 +221,7 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
       for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(Li + qb * 32 + 8 * j + 4 * hh);
+          const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(Li + (qb * 4 + j) * 16 + 4 * hh);
 #pragma unroll
           for (int i = 0; i < 4; ++i) sp[qb][4 * j + i] = l4[i];
         }
@@ -218,19 +245,25 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
         acc[i % NDB] = mfma32<DT>(op[(i / NDB / 2) % QB][(i / NDB) % 2], b, acc[i % NDB]);
         __builtin_amdgcn_sched_barrier(0);
       }
+      side(i);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
   // the block for runtime flags (chain A: current tile, chain B: previous tile)
   auto run_block = [&](bool cur, bool prev, const float* Li, const uint16_t* A, const u16x8_t (&kv)[NKS],
                        f32x16_t (&sp)[QB], const uint16_t* B, const u16x8_t (&op)[QB][2],
-                       f32x16_t (&acc)[NDB]) __attribute__((always_inline)) {
+                       f32x16_t (&acc)[NDB], auto&& side) __attribute__((always_inline)) {
     // the wave in its MFMA block issues ahead of its partner's element-wise
     // phase on the shared SIMD
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_setprio(1);
-    if (cur && prev) block(std::true_type{}, std::true_type{}, Li, A, kv, sp, B, op, acc);
-    else if (cur) block(std::true_type{}, std::false_type{}, Li, A, kv, sp, B, op, acc);
-    else if (prev) block(std::false_type{}, std::true_type{}, Li, A, kv, sp, B, op, acc);
+    if (cur && prev) block(std::true_type{}, std::true_type{}, Li, A, kv, sp, B, op, acc, side);
+    else if (cur) block(std::true_type{}, std::false_type{}, Li, A, kv, sp, B, op, acc, side);
+    else if (prev) block(std::false_type{}, std::true_type{}, Li, A, kv, sp, B, op, acc, side);
+    else {
+#pragma unroll
+      for (int i = 0; i < NKS * QB; ++i) side(i);
+    }
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_setprio(0);
     __builtin_amdgcn_sched_barrier(0);
@@ -264,8 +297,8 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
     // role P, tile t in stage (Qc, Lc), previous tile's dO in Gp:
     //   X_t and dV += P_prev^T dO_prev in one block, then P_t -> op and LDS
     auto p_step = [&](const uint16_t* Qc, const float* Lc, const uint16_t* Gp, Cur t, bool cur,
-                      bool prev) __attribute__((always_inline)) {
-      run_block(cur, prev, Lc, Qc, kv, sp, Gp, op, acc);
+                      bool prev, auto&& side) __attribute__((always_inline)) {
+      run_block(cur, prev, Lc, Qc, kv, sp, Gp, op, acc, side);
       if (!cur) return;
       const bool is_self = t.g < G;
       const int sq0 = is_self ? self_begin + t.s * kRows : 0;
@@ -310,7 +343,7 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
             }
         }
       }
-      run_block(cur, prev, Lc + kRows, Gc, kv, sp, Qp, op, acc);
+      run_block(cur, prev, Lc + 8, Gc, kv, sp, Qp, op, acc, [](int) {});
     };
     // one tile: stage c holds tile tc, stage p the tile before (computed when
     // pv), stage n receives the next tile; afterwards this wave's loads of
@@ -321,11 +354,19 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
     auto step = [&](uint16_t* Qp, uint16_t* Gp, float* Lp, uint16_t* Qc, uint16_t* Gc, float* Lc,
                     uint16_t* Qn, uint16_t* Gn, float* Ln) __attribute__((always_inline)) {
       const Cur tn = cur_next(tc);
-      dma(Qn, Gn, Ln, tn);
-      __builtin_amdgcn_sched_barrier(0);  // the next tile's loads go out first
       const bool cur = tc.it < it_hi && !skipped(tc);
-      if constexpr (ROLE_P) p_step(Qc, Lc, Gp, tc, cur, pv);
-      else d_step(Gc, Lc, Qp, tc, cur, pv);
+      if constexpr (ROLE_P) {
+        // role P spreads the next tile's loads over its MFMA block
+        const Plan pl = plan(tn);
+        p_step(Qc, Lc, Gp, tc, cur, pv, [&](int i) __attribute__((always_inline)) {
+          if (i >= kDmaAt && (i - kDmaAt) % 2 == 0 && (i - kDmaAt) / 2 < kPieces)
+            piece(pl, (i - kDmaAt) / 2, Qn, Gn, Ln);
+        });
+      } else {
+        dma(Qn, Gn, Ln, tn);
+        __builtin_amdgcn_sched_barrier(0);  // the next tile's loads go out first
+        d_step(Gc, Lc, Qp, tc, cur, pv);
+      }
       pv = cur;
       tc = tn;
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
