@@ -306,17 +306,24 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
       auto to_p = [&](auto mask_tag) __attribute__((always_inline)) {
         constexpr bool MASK = decltype(mask_tag)::value;
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb)
+        for (int qb = 0; qb < QB; ++qb) {
+          uint32_t w[8];  // packed pairs (rows 8j + 4hh + 2m, + 1) at w[2j + m]
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int r0 = qb * 32 + 8 * j + 4 * hh;
+            float p[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              float p = fast_exp2(sp[qb][4 * j + i] * nc2);
-              if constexpr (MASK) p = (mykey < c_hi && (!is_self || mykey <= sq0 + r0 + i)) ? p : 0.0f;
-              op[qb][j >> 1][(j & 1) * 4 + i] = from_f32<DT>(p);
+              p[i] = fast_exp2(sp[qb][4 * j + i] * nc2);
+              if constexpr (MASK) p[i] = (mykey < c_hi && (!is_self || mykey <= sq0 + r0 + i)) ? p[i] : 0.0f;
             }
+            w[2 * j] = pack2<DT>(p[0], p[1]);
+            w[2 * j + 1] = pack2<DT>(p[2], p[3]);
           }
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2)
+            op[qb][h2] = __builtin_bit_cast(u16x8_t, (u32x4_t){w[4 * h2], w[4 * h2 + 1], w[4 * h2 + 2], w[4 * h2 + 3]});
+        }
       };
       if (need_mask) to_p(std::true_type{}); else to_p(std::false_type{});
 #pragma unroll
@@ -333,14 +340,19 @@ __global__ __launch_bounds__(512, 1) void dkdv2_kernel(BwdArgs a) {
         const int b = (t.it - 1) & 1;
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
-          const u16x8_t px[2] = {Px[b][pair][qb][0][lane], Px[b][pair][qb][1][lane]};
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
+          for (int h2 = 0; h2 < 2; ++h2) {
+            // word m of P row block h2: rows of sp elements 8 h2 + 2m, + 1
+            const u32x4_t pw = __builtin_bit_cast(u32x4_t, Px[b][pair][qb][h2][lane]);
+            uint32_t w[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int r = 4 * j + i, h2 = j >> 1, x = (j & 1) * 4 + i;
-              op[qb][h2][x] = from_f32<DT>(to_f32<DT>(px[h2][x]) * sp[qb][r]);
+            for (int m = 0; m < 4; ++m) {
+              float lo, hi;
+              unpack2<DT>(pw[m], lo, hi);
+              w[m] = pack2<DT>(lo * sp[qb][8 * h2 + 2 * m], hi * sp[qb][8 * h2 + 2 * m + 1]);
             }
+            op[qb][h2] = __builtin_bit_cast(u16x8_t, (u32x4_t){w[0], w[1], w[2], w[3]});
+          }
         }
       }
       run_block(cur, prev, Lc + 8, Gc, kv, sp, Qp, op, acc, [](int) {});

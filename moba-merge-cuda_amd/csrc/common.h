@@ -17,6 +17,7 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint16_t u16x8_t __attribute__((ext_vector_type(8)));
 typedef uint16_t u16x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 namespace moba {
 
@@ -50,6 +51,29 @@ template <int DT> MOBA_DEV float to_f32(uint16_t v) {
 template <int DT> MOBA_DEV uint16_t from_f32(float v) {
   if constexpr (DT == 0) return __builtin_bit_cast(uint16_t, (__bf16)v);
   else return f32_to_f16(v);
+}
+
+// Two floats to two packed 16-bit values, a in the low half: one
+// v_cvt_pk_* instruction (same rounding as from_f32).
+template <int DT> MOBA_DEV uint32_t pack2(float a, float b) {
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  if constexpr (DT == 0) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
+  } else {
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, f16x2_t));
+  }
+}
+// The two 16-bit values of a packed word as floats (low half first).
+template <int DT> MOBA_DEV void unpack2(uint32_t w, float& lo, float& hi) {
+  if constexpr (DT == 0) {
+    lo = __uint_as_float(w << 16);
+    hi = __uint_as_float(w & 0xffff0000u);
+  } else {
+    lo = to_f32<1>((uint16_t)(w & 0xffffu));
+    hi = to_f32<1>((uint16_t)(w >> 16));
+  }
 }
 
 // 32x32x16 MFMA on 8 packed 16-bit elements per lane.
@@ -91,9 +115,8 @@ MOBA_DEV u16x8_t zero8() {
 
 // sign flip of 8 bf16 / fp16 values (exact)
 MOBA_DEV u16x8_t neg8(u16x8_t x) {
-#pragma unroll
-  for (int i = 0; i < 8; ++i) x[i] ^= 0x8000;
-  return x;
+  const u32x4_t m = {0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
+  return __builtin_bit_cast(u16x8_t, __builtin_bit_cast(u32x4_t, x) ^ m);
 }
 
 MOBA_DEV u16x8_t ld8(const uint16_t* p) { return *reinterpret_cast<const u16x8_t*>(p); }
