@@ -1011,7 +1011,7 @@ extern "C" int moba_hip_prefill_bwd(const void* q, const void* k, const void* v,
     a.part_dkv = (float*)(ws + dkdv_sched_bytes(n_kv_tiles, kv_splits));
   }
   a.dq = (uint16_t*)dq; a.dk = (uint16_t*)dk; a.dv = (uint16_t*)dv;
-  a.lse_k = delta + (int64_t)T * Hq;
+  a.lse_k = delta + (int64_t)T * Hq;  // adjacent to delta (one load per row in the key-major kernels)
   a.pack_rows = (R > 0 && D <= 128) ? (int64_t)T * Hq * R : 0;
   a.pack_q = (uint16_t*)pack;
   a.pack_g = a.pack_q + a.pack_rows * D;

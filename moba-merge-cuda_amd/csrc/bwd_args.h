@@ -27,6 +27,9 @@ struct BwdArgs {
   const int* row_off;
   const int* counts;
   const int* rows;
+  // delta and lse_k are one allocation, lse_k = delta + T*Hq (the key-major
+  // kernels fetch both of a row with one load); likewise pack_delta =
+  // pack_lse_k + pack_rows
   float* delta;      // [T*Hq] rowsum(dO * O)
   float* lse_k;      // [T*Hq] lse / scale: the row's log-sum-exp in q.k units
   uint16_t* part_dq;  // remote dQ slots, input dtype
