@@ -116,7 +116,7 @@ int moba_hip_prefill_fwd(const void* q, const void* k, const void* v, int dtype,
  * keys; chunk -1 marks an empty entry.  delta [2*T*Hq] and
  * part_dq [T*Hq*R, D] (dtype) are workspaces.  pack is a workspace of
  * T*Hq*R*(4*D + 8) bytes, required when R > 0 and D <= 128 (the expert rows
- * of q, dO, lse and delta copied contiguously by the parts-1 launches and read
+ * of q, dO, lse / scale and delta copied contiguously by the parts-1 launches and read
  * by the key-major kernel: pass the same buffer to both calls), else may be
  * NULL.  dq [T,Hq,D], dk/dv [T,Hkv,D] (dtype) are fully written (every key
  * belongs to exactly one kv tile).
