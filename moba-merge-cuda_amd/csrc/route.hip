@@ -19,7 +19,7 @@ namespace {
 
 constexpr int kMaxRemote = 8;
 
-// One workgroup per (filtered chunk, kv head).  The mean of dim d is the
+// One workgroup per (filtered chunk, kv head, dim slice of D / ds).  The mean of dim d is the
 // canonical sum: 64 partial sums s_j over the tokens j, j+64, j+128, ... in
 // increasing order, then the fixed tree canon_tree over j.  Work item
 // (j, column block b) of 8 dims is p = j * nd8 + b, so a wave's loads cover
@@ -28,11 +28,12 @@ constexpr int kMaxRemote = 8;
 template <int DT, int NP>
 __global__ __launch_bounds__(256) void chunk_means_kernel(const uint16_t* __restrict__ k, int Hkv,
                                                           int D, const int* __restrict__ chunk_start,
-                                                          int C, int precision,
+                                                          int C, int precision, int ds,
                                                           float* __restrict__ means) {
   extern __shared__ float part[];  // [64][D]
-  const int nd8 = D / 8, np = 64 * nd8;
-  const int kh = blockIdx.x % Hkv, f = blockIdx.x / Hkv;
+  const int nd8 = D / 8 / ds, np = 64 * nd8;  // this workgroup's 8-dim blocks
+  const int sub = blockIdx.x % ds, fk = blockIdx.x / ds;
+  const int kh = fk % Hkv, f = fk / Hkv;
   const int tid = threadIdx.x;
   const int64_t stride = (int64_t)Hkv * D;
   const uint16_t* base = k + ((int64_t)chunk_start[f] * Hkv + kh) * D;
@@ -42,23 +43,31 @@ __global__ __launch_bounds__(256) void chunk_means_kernel(const uint16_t* __rest
   for (int i = 0; i < NP; ++i) {
     const int p = tid + 256 * i;
     jj[i] = p < np ? p / nd8 : C;  // items past np load nothing
-    bb[i] = p % nd8;
+    bb[i] = sub * nd8 + p % nd8;
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[i][e] = 0.0f;
   }
-  for (int t0 = 0; t0 < C; t0 += 64) {
-    u16x8_t x[NP];
+  // KU row groups of 64 tokens per pass: all their loads are issued before
+  // the adds, which then run in token order (one load latency per pass, not
+  // per group)
+  constexpr int KU = NP <= 2 ? 8 : 4;
+  for (int t0 = 0; t0 < C; t0 += 64 * KU) {
+    u16x8_t x[KU][NP];
 #pragma unroll
-    for (int i = 0; i < NP; ++i) {
-      const int t = t0 + jj[i];
-      x[i] = t < C ? ld8(base + t * stride + bb[i] * 8) : zero8();
-    }
+    for (int u = 0; u < KU; ++u)
 #pragma unroll
-    for (int i = 0; i < NP; ++i)
-      if (t0 + jj[i] < C) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[i][e] = acc[i][e] + to_f32<DT>(x[i][e]);
+      for (int i = 0; i < NP; ++i) {
+        const int t = t0 + 64 * u + jj[i];
+        x[u][i] = t < C ? ld8(base + t * stride + bb[i] * 8) : zero8();
       }
+#pragma unroll
+    for (int u = 0; u < KU; ++u)
+#pragma unroll
+      for (int i = 0; i < NP; ++i)
+        if (t0 + 64 * u + jj[i] < C) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[i][e] = acc[i][e] + to_f32<DT>(x[u][i][e]);
+        }
   }
 #pragma unroll
   for (int i = 0; i < NP; ++i) {
@@ -71,7 +80,7 @@ __global__ __launch_bounds__(256) void chunk_means_kernel(const uint16_t* __rest
   __syncthreads();
   const int lane = tid & 63, w = tid >> 6;
   float* dst = means + ((int64_t)f * Hkv + kh) * D;
-  for (int d = w; d < D; d += 4) {
+  for (int d = sub * nd8 * 8 + w; d < (sub + 1) * nd8 * 8; d += 4) {
     float m = canon_tree(part[lane * D + d]) / (float)C;
     if (precision == 0) m = to_f32<DT>(from_f32<DT>(m));
     if (lane == 0) dst[d] = m;
@@ -109,12 +118,28 @@ __global__ __launch_bounds__(256) void route_kernel(const uint16_t* __restrict__
   const int h = blockIdx.y;
   const bool live = s < T;
   const int G = Hq / Hkv, kh = h / G;
+  // the q row first: its loads overlap the chunk search below
+  const int64_t idx = (int64_t)s * Hq + h;
+  constexpr int NQ = DP / 8;
+  u16x8_t qv[NQ];
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) qv[i] = (live && i * 8 < D) ? ld8(q + idx * D + i * 8) : zero8();
   // chunk containing s (the last token's for the threads past T)
   const int sc = live ? s : T - 1;
+  // search once per wave for its first token (uniform loads), then per lane
+  // only when the wave straddles a chunk boundary
+  const int sw = __builtin_amdgcn_readfirstlane(sc);
   int lo = 0, hi = nchunk - 1;
   while (lo < hi) {
     int mid = (lo + hi + 1) >> 1;
-    if (cu_chunk[mid] <= sc) lo = mid; else hi = mid - 1;
+    if (cu_chunk[mid] <= sw) lo = mid; else hi = mid - 1;
+  }
+  if (__ballot(sc >= cu_chunk[lo + 1]) != 0) {
+    lo = 0; hi = nchunk - 1;
+    while (lo < hi) {
+      int mid = (lo + hi + 1) >> 1;
+      if (cu_chunk[mid] <= sc) lo = mid; else hi = mid - 1;
+    }
   }
   const int cs = lo, b = chunk_batch[cs], c0 = first_chunk[cs];
   // this thread's candidates are filtered rows [c0 - b, cs - b)
@@ -131,12 +156,7 @@ __global__ __launch_bounds__(256) void route_kernel(const uint16_t* __restrict__
   const int flo = min(min(red[0][0], red[0][1]), min(red[0][2], red[0][3]));
   const int fhi = max(max(red[1][0], red[1][1]), max(red[1][2], red[1][3]));
 
-  const int64_t idx = (int64_t)s * Hq + h;
-  constexpr int NQ = DP / 8;
   constexpr bool QF32 = DP <= 128;      // q row as fp32 registers
-  u16x8_t qv[NQ];
-#pragma unroll
-  for (int i = 0; i < NQ; ++i) qv[i] = (live && i * 8 < D) ? ld8(q + idx * D + i * 8) : zero8();
   float qf[QF32 ? DP : 1];
   if constexpr (QF32) {
 #pragma unroll
@@ -402,14 +422,20 @@ extern "C" int moba_hip_chunk_means(const void* k, int dtype, int T, int Hkv, in
   if (dtype != 0 && dtype != 1) { moba_set_error("chunk_means: dtype must be 0 (bf16) or 1 (fp16)"); return MOBA_ERR_ARG; }
   if (D < 8 || D % 8 || Hkv < 1 || chunk < 1) { moba_set_error("chunk_means: bad shape"); return MOBA_ERR_ARG; }
   if (D > 256) { moba_set_error("chunk_means: head_dim must be at most 256"); return MOBA_ERR_ARG; }
-  dim3 grid((unsigned)((int64_t)F * Hkv)), block(256);
+  // dim slices per (chunk, kv head), until the grid has about 512 workgroups,
+  // each slice at least 128 bytes of a key row (whole 128-byte lines; 64 when
+  // there are fewer than 64 (chunk, kv head) pairs)
+  int ds = 1;
+  const int64_t wgs = (int64_t)F * Hkv;
+  while ((D / 8) % (2 * ds) == 0 && D / 8 / (2 * ds) >= (wgs < 64 ? 4 : 8) && wgs * ds < 512) ds *= 2;
+  dim3 grid((unsigned)((int64_t)F * Hkv * ds)), block(256);
   const size_t lds = (size_t)64 * D * sizeof(float);
   hipStream_t st = (hipStream_t)stream;
   const uint16_t* kp = (const uint16_t*)k;
 #define MOBA_MEANS(DT_, NP_) \
   hipLaunchKernelGGL((chunk_means_kernel<DT_, NP_>), grid, block, lds, st, kp, Hkv, D, chunk_start, \
-                     chunk, precision, means)
-  const int nd8 = D / 8;
+                     chunk, precision, ds, means)
+  const int nd8 = D / 8 / ds;
   if (dtype == 0) {
     if (nd8 <= 4) MOBA_MEANS(0, 1); else if (nd8 <= 8) MOBA_MEANS(0, 2);
     else if (nd8 <= 16) MOBA_MEANS(0, 4); else MOBA_MEANS(0, 8);
